@@ -1,0 +1,607 @@
+// Paged block-masked attention for gfx950 (MI355X).
+//
+// out[q, h] = sum_j softmax_j(scale * q.k_j + mask) v_j over the keys of one
+// sequence, the keys living in 16-slot pages of a bf16 pool (layout in
+// emb_kv.h).  Reference semantics: runtime_kv_attn_* over valid slots
+// (kernels/lingbot/lingbot_flex_attn_cuda.cu:651-873), flex_attn with a CSR
+// block table and token mask (:502-582), and the ggml attention the VLA
+// experts call (models/pi05.cpp:405-418, models/hy_vla.cpp:1066-1076) with
+// GQA broadcast (q head h reads kv head h / (hq/hkv)).
+//
+// Work decomposition.  A workgroup of 4 waves owns 128 query rows of one
+// (sequence, kv head); a row is (token, q head of the GQA group), so all query
+// heads that share a kv head also share every K/V tile the workgroup stages in
+// LDS.  Each wave owns 32 rows.  Keys stream in tiles of 32 (two pages).
+//
+// Per wave and key tile the math is done transposed, with MFMA 32x32x16:
+//   S^T[32 keys x 32 rows] = K[keys x D] . Q^T       (bf16 x bf16 -> f32)
+//   O^T[D x 32 rows]      += V^T[D x keys] . P^T      (f16 x f16 -> f32)
+// so that lane l owns query row l%32: its 16 scores and its D/2 output
+// accumulators all belong to the same row, the row max needs one cross-lane
+// step (lanes l and l^32), and rescaling needs no shuffles.  P and V go through
+// f16 rather than bf16 because P in bf16 (8 significant bits) alone would put
+// the mean relative error near 1.6e-3; f16 keeps it near 2e-4.  V is converted
+// bf16 -> f16 while it is staged in LDS (exact for |v| in [2^-14, 65504]).
+//
+// The online softmax works in log2 units and rescales the accumulators only
+// when a row max grows by more than 2^8, so most tiles skip the rescale.
+//
+// Split-K: with splits > 1 each workgroup handles one key range and writes
+// unnormalised partials (O, m, l) that attn_merge_kernel combines.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+
+#include "emb_common.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int WAVES = 4;
+constexpr int ROWS_PER_WAVE = 32;
+constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
+constexpr int KT = 32;          // keys per tile (two pages)
+constexpr float RESCALE_TH = 8.0f;  // log2 units
+constexpr float LOG2E = 1.4426950408889634f;
+
+struct KParams {
+    const void *q;
+    float *out;
+    int64_t q_stride, out_stride;
+    const int32_t *cu_q;
+    const int32_t *n_keys;
+    const int32_t *q_pos0;
+    int32_t nq_single, nk_single;  // used when cu_q / n_keys are null (batch 1)
+    const uint16_t *k_pool;
+    const uint16_t *v_pool;
+    const int32_t *bt;
+    int32_t bt_stride;
+    const int32_t *valid;
+    int32_t valid_stride;
+    int32_t capacity;
+    int32_t batch, hq, hkv, G;
+    int32_t row_tiles;
+    int32_t splits;
+    int32_t total_wg;
+    float scale_log2;
+    int32_t chunk, window;
+    const void *mask;
+    int64_t mask_q_stride, mask_b_stride;
+    const uint8_t *bmap;
+    int32_t bsize, bmap_cols;
+    int64_t bmap_b_stride;
+    float *ws_o;   // [batch*hkv][splits][row_tiles*128][D]
+    float *ws_ml;  // [batch*hkv][splits][row_tiles*128][2]
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// Two bf16 (packed in a dword) -> two f16 (packed in a dword), round to nearest even.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
+    const _Float16 lo = (_Float16)bf16_to_f32(w & 0xffffu);
+    const _Float16 hi = (_Float16)bf16_to_f32(w >> 16);
+    return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+template <int D>
+struct Smem {
+    static constexpr int KS_STRIDE = D + 8;    // bf16 elements per staged key row
+    static constexpr int VS_STRIDE = KT + 8;   // f16 elements per staged dim row
+    uint16_t ks[KT * KS_STRIDE];
+    uint16_t vs[D * VS_STRIDE];
+};
+
+template <bool VALID>
+__device__ __forceinline__ int32_t key_slot(const KParams &p, const int32_t *valid_b, int32_t j, int32_t nk) {
+    if (j >= nk) return -2;  // beyond the key list: zero row, masked
+    if (!VALID) return j;
+    return valid_b[j];
+}
+
+__device__ __forceinline__ int64_t page_of(const int32_t *bt_b, int32_t slot) {
+    return bt_b ? (int64_t)bt_b[slot >> 4] : (int64_t)(slot >> 4);
+}
+
+// Stages keys [k0, k0+32) into LDS: K rows as bf16, V as f16 in the transposed,
+// key-permuted layout the PV MFMA reads (within a page, key t sits at position
+// t with bits 2 and 3 swapped).
+template <int D, bool VALID>
+__device__ __forceinline__ void stage_tile(const KParams &p, Smem<D> &sm, const int32_t *valid_b,
+                                           const int32_t *bt_b, int32_t k0, int32_t nk, int32_t kvh) {
+    constexpr int CH = D / 8;  // 16-byte chunks per key row
+    const int tid = threadIdx.x;
+    // K: KT keys x CH chunks
+#pragma unroll
+    for (int it = 0; it < (KT * CH) / 256; ++it) {
+        const int c = tid + it * 256;
+        const int key = c / CH, dc = c % CH;
+        const int32_t slot = key_slot<VALID>(p, valid_b, k0 + key, nk);
+        u32x4 w = {0u, 0u, 0u, 0u};
+        if (slot >= 0 && slot < p.capacity) {
+            const int64_t page = page_of(bt_b, slot);
+            if (page >= 0)
+                w = *reinterpret_cast<const u32x4 *>(p.k_pool + ((page * p.hkv + kvh) * 16 + (slot & 15)) * D + dc * 8);
+        }
+        *reinterpret_cast<u32x4 *>(&sm.ks[key * Smem<D>::KS_STRIDE + dc * 8]) = w;
+    }
+    // V: 2 pages x D dims x 2 halves of 8 keys
+#pragma unroll
+    for (int it = 0; it < (4 * D) / 256; ++it) {
+        const int c = tid + it * 256;
+        const int pg = c / (2 * D);
+        const int rem = c % (2 * D);
+        const int d = rem >> 1, half = rem & 1;
+        const int jb = k0 + pg * 16 + half * 8;  // first key of these 8
+        u32x4 w = {0u, 0u, 0u, 0u};
+        const int32_t s0 = key_slot<VALID>(p, valid_b, jb, nk);
+        bool fast = s0 >= 0 && (s0 & 7) == 0 && s0 + 7 < p.capacity && jb + 7 < nk;
+        if (VALID && fast) {
+#pragma unroll
+            for (int e = 1; e < 8; ++e) fast = fast && valid_b[jb + e] == s0 + e;
+        }
+        if (fast) {
+            const int64_t page = page_of(bt_b, s0);
+            if (page >= 0)
+                w = *reinterpret_cast<const u32x4 *>(p.v_pool + ((page * p.hkv + kvh) * D + d) * 16 + (s0 & 15));
+        } else {
+            uint32_t hv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int32_t s = key_slot<VALID>(p, valid_b, jb + e, nk);
+                hv[e] = 0u;
+                if (s >= 0 && s < p.capacity) {
+                    const int64_t page = page_of(bt_b, s);
+                    if (page >= 0) hv[e] = p.v_pool[((page * p.hkv + kvh) * D + d) * 16 + (s & 15)];
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = hv[2 * e] | (hv[2 * e + 1] << 16);
+        }
+        u32x2 lo = {bf16x2_to_f16x2(w[0]), bf16x2_to_f16x2(w[1])};  // keys +0..3
+        u32x2 hi = {bf16x2_to_f16x2(w[2]), bf16x2_to_f16x2(w[3])};  // keys +4..7
+        uint16_t *row = &sm.vs[d * Smem<D>::VS_STRIDE + pg * 16];
+        *reinterpret_cast<u32x2 *>(row + half * 4) = lo;
+        *reinterpret_cast<u32x2 *>(row + 8 + half * 4) = hi;
+    }
+}
+
+template <int D, int MASK, bool VALID, bool QF32>
+__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void paged_attn_kernel(KParams p) {
+    __shared__ Smem<D> sm;
+
+    // XCD-aware order: hardware ids go round-robin over the 8 XCDs, so logical
+    // work ids are handed out in contiguous runs per XCD, keeping the row tiles
+    // of one (sequence, kv head) -- which read the same K/V -- on one L2.
+    const int nwg_pad = (int)gridDim.x;
+    const int lin = (int)(blockIdx.x % 8) * (nwg_pad / 8) + (int)(blockIdx.x / 8);
+    if (lin >= p.total_wg) return;
+    const int row_tile = lin % p.row_tiles;
+    int rest = lin / p.row_tiles;
+    const int split = rest % p.splits;
+    rest /= p.splits;
+    const int kvh = rest % p.hkv;
+    const int b = rest / p.hkv;
+
+    const int32_t q_begin = p.cu_q ? p.cu_q[b] : 0;
+    const int32_t nq = p.cu_q ? p.cu_q[b + 1] - q_begin : p.nq_single;
+    const int32_t nk = p.n_keys ? p.n_keys[b] : p.nk_single;
+    const int32_t rows = nq * p.G;
+    const int32_t row0 = row_tile * ROWS_PER_WG;
+    if (row0 >= rows) return;
+    const int32_t qpos0 = p.q_pos0 ? p.q_pos0[b] : nk - nq;
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int lrow = lane & 31;
+    const int lhi = lane >> 5;
+    const int32_t my_row = row0 + wave * ROWS_PER_WAVE + lrow;
+    const bool row_ok = my_row < rows;
+    const int32_t tok = row_ok ? my_row / p.G : 0;
+    const int32_t head = kvh * p.G + (row_ok ? my_row % p.G : 0);
+    const int32_t qpos = qpos0 + tok;
+
+    const int32_t *valid_b = VALID ? p.valid + (int64_t)b * p.valid_stride : nullptr;
+    const int32_t *bt_b = p.bt ? p.bt + (int64_t)b * p.bt_stride : nullptr;
+
+    // Query fragment: B operand of S^T = K Q^T.  Lane l holds row l%32,
+    // dims kk*16 + (l/32)*8 + [0, 8).
+    bf16x8 qf[D / 16];
+    {
+        const int64_t qoff = (int64_t)(q_begin + tok) * p.q_stride + (int64_t)head * D + lhi * 8;
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+            u32x4 w = {0u, 0u, 0u, 0u};
+            if (row_ok) {
+                if (QF32) {
+                    const float *qp = reinterpret_cast<const float *>(p.q) + qoff + kk * 16;
+                    const f32x4 a = *reinterpret_cast<const f32x4 *>(qp);
+                    const f32x4 c = *reinterpret_cast<const f32x4 *>(qp + 4);
+                    w[0] = f32_to_bf16_bits(a[0]) | (f32_to_bf16_bits(a[1]) << 16);
+                    w[1] = f32_to_bf16_bits(a[2]) | (f32_to_bf16_bits(a[3]) << 16);
+                    w[2] = f32_to_bf16_bits(c[0]) | (f32_to_bf16_bits(c[1]) << 16);
+                    w[3] = f32_to_bf16_bits(c[2]) | (f32_to_bf16_bits(c[3]) << 16);
+                } else {
+                    w = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(p.q) + qoff + kk * 16);
+                }
+            }
+            qf[kk] = __builtin_bit_cast(bf16x8, w);
+        }
+    }
+
+    // Key range of this workgroup: mask bounds, then this split's share.
+    int32_t k_lo = 0, k_hi = nk;
+    if (MASK == EMB_MASK_CHUNK) {
+        const int32_t last_row = min(row0 + ROWS_PER_WG, rows) - 1;
+        const int32_t qp_min = qpos0 + row0 / p.G, qp_max = qpos0 + last_row / p.G;
+        k_hi = min(nk, (qp_max / p.chunk + 1) * p.chunk);
+        if (p.window >= 0) k_lo = max(0, (qp_min / p.chunk - p.window) * p.chunk);
+    }
+    int32_t t_lo = k_lo / KT, t_hi = (max(k_hi, k_lo) + KT - 1) / KT;
+    if (p.splits > 1) {
+        const int32_t nt = t_hi - t_lo;
+        const int32_t per = (nt + p.splits - 1) / p.splits;
+        const int32_t a = t_lo + split * per;
+        t_hi = min(t_hi, a + per);
+        t_lo = min(a, t_hi);
+    }
+
+    f32x16 acc_o[D / 32];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) acc_o[i] = f32x16{};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    for (int32_t t = t_lo; t < t_hi; ++t) {
+        const int32_t k0 = t * KT;
+        __syncthreads();
+        stage_tile<D, VALID>(p, sm, valid_b, bt_b, k0, nk, kvh);
+        __syncthreads();
+
+        // S^T = K Q^T : lane holds keys (r/4)*8 + lhi*4 + r%4 of row lrow.
+        f32x16 s = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+            const u32x4 kw =
+                *reinterpret_cast<const u32x4 *>(&sm.ks[lrow * Smem<D>::KS_STRIDE + kk * 16 + lhi * 8]);
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kw), qf[kk], s, 0, 0, 0);
+        }
+
+        // scale, mask, tile max
+        float mt = -INFINITY;
+        const bool tile_full = (MASK == EMB_MASK_FULL) && (k0 + KT <= nk);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int32_t j = k0 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+            float x = s[r] * p.scale_log2;
+            if (!tile_full) {
+                bool vis = row_ok && j < nk;
+                if (MASK == EMB_MASK_CHUNK) {
+                    const int32_t qc = qpos / p.chunk, kc = j / p.chunk;
+                    vis = vis && kc <= qc && (p.window < 0 || qc - kc <= p.window);
+                } else if (MASK == EMB_MASK_TOKEN) {
+                    vis = vis && reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                          (int64_t)tok * p.mask_q_stride + j] != 0;
+                } else if (MASK == EMB_MASK_ADD) {
+                    if (vis)
+                        x += LOG2E * reinterpret_cast<const float *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                             (int64_t)tok * p.mask_q_stride + j];
+                } else if (MASK == EMB_MASK_BLOCKMAP) {
+                    vis = vis && p.bmap[(int64_t)b * p.bmap_b_stride + (int64_t)(tok / p.bsize) * p.bmap_cols +
+                                        j / p.bsize] != 0;
+                    if (vis && p.mask)
+                        vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                        (int64_t)tok * p.mask_q_stride + j] != 0;
+                }
+                if (!vis) x = -INFINITY;
+            }
+            s[r] = x;
+            mt = fmaxf(mt, x);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        if (mt > m_run + RESCALE_TH) {
+            const float alpha = __builtin_amdgcn_exp2f(m_run - mt);  // m_run = -inf -> 0
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
+            l_run *= alpha;
+            m_run = mt;
+        }
+        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+        f16x8 pf[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float e = __builtin_amdgcn_exp2f(s[r] - m_use);
+            l_run += e;
+            pf[r >> 3][r & 7] = (_Float16)e;
+        }
+
+        // O^T += V^T P^T, one 16-key page per MFMA step.
+#pragma unroll
+        for (int pg = 0; pg < 2; ++pg) {
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const u32x4 vw = *reinterpret_cast<const u32x4 *>(
+                    &sm.vs[(dt * 32 + lrow) * Smem<D>::VS_STRIDE + pg * 16 + lhi * 8]);
+                acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vw), pf[pg],
+                                                                  acc_o[dt], 0, 0, 0);
+            }
+        }
+    }
+
+    l_run += __shfl_xor(l_run, 32);
+    if (!row_ok) return;
+
+    if (p.splits > 1) {
+        const int64_t unit = (int64_t)(b * p.hkv + kvh) * p.splits + split;
+        const int64_t rowi = unit * ((int64_t)p.row_tiles * ROWS_PER_WG) + my_row;
+        float *wo = p.ws_o + rowi * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f32x4 v = {acc_o[dt][j * 4], acc_o[dt][j * 4 + 1], acc_o[dt][j * 4 + 2], acc_o[dt][j * 4 + 3]};
+                *reinterpret_cast<f32x4 *>(wo + dt * 32 + j * 8 + lhi * 4) = v;
+            }
+        if (lhi == 0) {
+            p.ws_ml[rowi * 2] = m_run;
+            p.ws_ml[rowi * 2 + 1] = l_run;
+        }
+        return;
+    }
+
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    float *op = p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f32x4 v = {acc_o[dt][j * 4] * inv, acc_o[dt][j * 4 + 1] * inv, acc_o[dt][j * 4 + 2] * inv,
+                       acc_o[dt][j * 4 + 3] * inv};
+            *reinterpret_cast<f32x4 *>(op + dt * 32 + j * 8 + lhi * 4) = v;
+        }
+}
+
+// Combines split partials: m = max m_s, l = sum l_s 2^(m_s - m),
+// out = sum O_s 2^(m_s - m) / l.  One thread per (row, 4 dims).
+template <int D>
+__global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
+    const int64_t rows_per_unit = (int64_t)p.row_tiles * ROWS_PER_WG;
+    const int64_t total = (int64_t)p.batch * p.hkv * rows_per_unit * (D / 4);
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int d4 = (int)(idx % (D / 4));
+        int64_t r = idx / (D / 4);
+        const int32_t row = (int32_t)(r % rows_per_unit);
+        r /= rows_per_unit;
+        const int kvh = (int)(r % p.hkv);
+        const int b = (int)(r / p.hkv);
+        const int32_t q_begin = p.cu_q ? p.cu_q[b] : 0;
+        const int32_t nq = p.cu_q ? p.cu_q[b + 1] - q_begin : p.nq_single;
+        if (row >= nq * p.G) continue;
+        const int64_t unit0 = (int64_t)(b * p.hkv + kvh) * p.splits;
+        float m = -INFINITY;
+        for (int s = 0; s < p.splits; ++s) m = fmaxf(m, p.ws_ml[((unit0 + s) * rows_per_unit + row) * 2]);
+        const float m_use = m == -INFINITY ? 0.0f : m;
+        float l = 0.0f;
+        f32x4 o = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < p.splits; ++s) {
+            const int64_t ri = (unit0 + s) * rows_per_unit + row;
+            const float w = __builtin_amdgcn_exp2f(p.ws_ml[ri * 2] - m_use);
+            l += w * p.ws_ml[ri * 2 + 1];
+            const f32x4 x = *reinterpret_cast<const f32x4 *>(p.ws_o + ri * D + d4 * 4);
+            o += w * x;
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        const int32_t tok = row / p.G;
+        const int32_t head = kvh * p.G + row % p.G;
+        *reinterpret_cast<f32x4 *>(p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + d4 * 4) =
+            o * inv;
+    }
+}
+
+template <int D, int MASK, bool VALID, bool QF32>
+hipError_t launch_kernel(const KParams &kp, hipStream_t stream) {
+    const int grid = (kp.total_wg + 7) / 8 * 8;
+    hipLaunchKernelGGL((paged_attn_kernel<D, MASK, VALID, QF32>), dim3(grid), dim3(256), 0, stream, kp);
+    return hipGetLastError();
+}
+
+template <int D, int MASK>
+hipError_t dispatch_vq(const KParams &kp, bool valid, bool qf32, hipStream_t stream) {
+    if (valid) return qf32 ? launch_kernel<D, MASK, true, true>(kp, stream) : launch_kernel<D, MASK, true, false>(kp, stream);
+    return qf32 ? launch_kernel<D, MASK, false, true>(kp, stream) : launch_kernel<D, MASK, false, false>(kp, stream);
+}
+
+template <int D>
+hipError_t dispatch_mask(const KParams &kp, int mask, bool valid, bool qf32, hipStream_t stream) {
+    switch (mask) {
+        case EMB_MASK_FULL: return dispatch_vq<D, EMB_MASK_FULL>(kp, valid, qf32, stream);
+        case EMB_MASK_CHUNK: return dispatch_vq<D, EMB_MASK_CHUNK>(kp, valid, qf32, stream);
+        case EMB_MASK_TOKEN: return dispatch_vq<D, EMB_MASK_TOKEN>(kp, valid, qf32, stream);
+        case EMB_MASK_ADD: return dispatch_vq<D, EMB_MASK_ADD>(kp, valid, qf32, stream);
+        default: return dispatch_vq<D, EMB_MASK_BLOCKMAP>(kp, valid, qf32, stream);
+    }
+}
+
+template <int D>
+hipError_t launch_merge(const KParams &kp, hipStream_t stream) {
+    const int64_t total = (int64_t)kp.batch * kp.hkv * kp.row_tiles * ROWS_PER_WG * (D / 4);
+    int64_t g = (total + 255) / 256;
+    if (g > 65536) g = 65536;
+    hipLaunchKernelGGL((attn_merge_kernel<D>), dim3((int)g), dim3(256), 0, stream, kp);
+    return hipGetLastError();
+}
+
+inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, hipStream_t stream) {
+    EMB_CHECK_ARG(a, "null args");
+    EMB_CHECK_ARG(a->q && a->out && a->k_pool && a->v_pool, "null q/out/pool");
+    EMB_CHECK_ARG(a->batch > 0 && a->hq > 0 && a->hkv > 0 && a->hq % a->hkv == 0, "bad head counts");
+    EMB_CHECK_ARG(a->head_dim == 64 || a->head_dim == 128 || a->head_dim == 256, "head_dim must be 64, 128 or 256");
+    EMB_CHECK_ARG(a->max_q > 0, "max_q must be positive");
+    EMB_CHECK_ARG((a->cu_q && a->n_keys) || (!a->cu_q && !a->n_keys && a->batch == 1),
+                  "cu_q and n_keys are required for batch > 1");
+    EMB_CHECK_ARG(a->capacity > 0, "capacity must be positive");
+    EMB_CHECK_ARG(!a->valid_slots || a->valid_stride >= 0, "bad valid_stride");
+    EMB_CHECK_ARG(!a->block_tables || a->bt_stride > 0, "bad bt_stride");
+    const int64_t esz = a->q_is_f32 ? 4 : 2;
+    EMB_CHECK_ARG(a->q_stride >= (int64_t)a->hq * a->head_dim && (a->q_stride * esz) % 16 == 0,
+                  "q_stride must cover a token and keep 16-byte alignment");
+    EMB_CHECK_ARG(a->out_stride >= (int64_t)a->hq * a->head_dim && a->out_stride % 4 == 0, "bad out_stride");
+    EMB_CHECK_ARG(aligned16(a->q) && aligned16(a->out) && aligned16(a->k_pool) && aligned16(a->v_pool),
+                  "buffers must be 16-byte aligned");
+    EMB_CHECK_ARG(a->mask_kind >= EMB_MASK_FULL && a->mask_kind <= EMB_MASK_BLOCKMAP, "unknown mask kind");
+    if (a->mask_kind == EMB_MASK_CHUNK) EMB_CHECK_ARG(a->chunk > 0, "chunk must be positive");
+    if (a->mask_kind == EMB_MASK_TOKEN || a->mask_kind == EMB_MASK_ADD) EMB_CHECK_ARG(a->mask, "mask pointer required");
+    if (a->mask_kind == EMB_MASK_BLOCKMAP)
+        EMB_CHECK_ARG(a->block_map && a->block_size > 0 && a->block_map_cols > 0, "block map required");
+    const int splits = a->splits > 1 ? a->splits : 1;
+    EMB_CHECK_ARG(splits <= 64, "splits must be <= 64");
+    if (splits > 1) EMB_CHECK_ARG(a->workspace && aligned16(a->workspace), "split-K needs an aligned workspace");
+
+    KParams kp{};
+    kp.q = a->q;
+    kp.out = a->out;
+    kp.q_stride = a->q_stride;
+    kp.out_stride = a->out_stride;
+    kp.cu_q = a->cu_q;
+    kp.n_keys = a->n_keys;
+    kp.q_pos0 = a->q_pos0;
+    kp.nq_single = nq_single;
+    kp.nk_single = nk_single;
+    kp.k_pool = (const uint16_t *)a->k_pool;
+    kp.v_pool = (const uint16_t *)a->v_pool;
+    kp.bt = a->block_tables;
+    kp.bt_stride = a->bt_stride;
+    kp.valid = a->valid_slots;
+    kp.valid_stride = a->valid_stride;
+    kp.capacity = a->capacity;
+    kp.batch = a->batch;
+    kp.hq = a->hq;
+    kp.hkv = a->hkv;
+    kp.G = a->hq / a->hkv;
+    kp.row_tiles = (int32_t)(((int64_t)a->max_q * kp.G + ROWS_PER_WG - 1) / ROWS_PER_WG);
+    kp.splits = splits;
+    const int64_t total = (int64_t)a->batch * a->hkv * splits * kp.row_tiles;
+    EMB_CHECK_ARG(total < INT_MAX / 2, "grid too large");
+    kp.total_wg = (int32_t)total;
+    kp.scale_log2 = a->scale * LOG2E;
+    kp.chunk = a->chunk;
+    kp.window = a->window;
+    kp.mask = a->mask;
+    kp.mask_q_stride = a->mask_q_stride;
+    kp.mask_b_stride = a->mask_batch_stride;
+    kp.bmap = a->block_map;
+    kp.bsize = a->block_size;
+    kp.bmap_cols = a->block_map_cols;
+    kp.bmap_b_stride = a->block_map_batch_stride;
+    if (splits > 1) {
+        const int64_t rows_all = (int64_t)a->batch * a->hkv * splits * kp.row_tiles * ROWS_PER_WG;
+        kp.ws_o = (float *)a->workspace;
+        kp.ws_ml = kp.ws_o + rows_all * a->head_dim;
+    }
+    const bool valid = a->valid_slots != nullptr;
+    const bool qf32 = a->q_is_f32 != 0;
+    hipError_t e;
+    switch (a->head_dim) {
+        case 64: e = dispatch_mask<64>(kp, a->mask_kind, valid, qf32, stream); break;
+        case 128: e = dispatch_mask<128>(kp, a->mask_kind, valid, qf32, stream); break;
+        default: e = dispatch_mask<256>(kp, a->mask_kind, valid, qf32, stream); break;
+    }
+    if (e == hipSuccess && splits > 1) {
+        switch (a->head_dim) {
+            case 64: e = launch_merge<64>(kp, stream); break;
+            case 128: e = launch_merge<128>(kp, stream); break;
+            default: e = launch_merge<256>(kp, stream); break;
+        }
+    }
+    if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "paged attention launch: %s", hipGetErrorString(e));
+    return EMB_OK;
+}
+
+// Reference-named face: q/out f32 [seq][H][D], cache buffers hold the bf16
+// identity-paged pool written by lingbot_runtime_kv_update_f32, MHA.
+int runtime_kv_attn(const float *q, const float *cache_k, const float *cache_v, const int *valid_slots, float *out,
+                    int seq_q, int seq_k, int n_heads, int head_dim, int capacity, float scale, hipStream_t stream) {
+    EMB_CHECK_ARG(q && cache_k && cache_v && valid_slots && out, "null pointer");
+    EMB_CHECK_ARG(seq_q > 0 && seq_k > 0 && n_heads > 0 && head_dim > 0, "non-positive size");
+    emb_attn_args a{};
+    a.q = q;
+    a.q_is_f32 = 1;
+    a.q_stride = (int64_t)n_heads * head_dim;
+    a.out = out;
+    a.out_stride = a.q_stride;
+    a.k_pool = cache_k;
+    a.v_pool = cache_v;
+    a.valid_slots = valid_slots;
+    a.valid_stride = 0;
+    a.capacity = capacity;
+    a.batch = 1;
+    a.hq = a.hkv = n_heads;
+    a.head_dim = head_dim;
+    a.max_q = seq_q;
+    a.scale = scale;
+    a.mask_kind = EMB_MASK_FULL;
+    return run_attention(&a, seq_q, seq_k, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_t hkv, int32_t head_dim,
+                                int32_t splits) {
+    if (batch <= 0 || max_q <= 0 || hq <= 0 || hkv <= 0 || hq % hkv || head_dim <= 0 || splits <= 1) return 0;
+    const int64_t row_tiles = ((int64_t)max_q * (hq / hkv) + ROWS_PER_WG - 1) / ROWS_PER_WG;
+    const int64_t rows_all = (int64_t)batch * hkv * splits * row_tiles * ROWS_PER_WG;
+    return (size_t)rows_all * (size_t)(head_dim + 2) * sizeof(float);
+}
+
+int emb_paged_attention(const emb_attn_args *a, hipStream_t stream) {
+    EMB_CHECK_ARG(a, "null args");
+    return run_attention(a, 0, 0, stream);
+}
+
+int lingbot_runtime_kv_attn_f32(const float *q, const float *cache_k, const float *cache_v, const int *valid_slots,
+                                float *out, int seq_q, int seq_k, int n_heads, int head_dim, float scale,
+                                hipStream_t stream) {
+    return runtime_kv_attn(q, cache_k, cache_v, valid_slots, out, seq_q, seq_k, n_heads, head_dim, INT_MAX, scale,
+                           stream);
+}
+
+int lingbot_runtime_kv_attn_online_f32(const float *q, const float *cache_k, const float *cache_v,
+                                       const int *valid_slots, float *out, int seq_q, int seq_k, int n_heads,
+                                       int head_dim, float scale, hipStream_t stream) {
+    return runtime_kv_attn(q, cache_k, cache_v, valid_slots, out, seq_q, seq_k, n_heads, head_dim, INT_MAX, scale,
+                           stream);
+}
+
+int lingbot_runtime_kv_attn_warp_f32(const float *q, const float *cache_k, const float *cache_v,
+                                     const int *valid_slots, float *out, int seq_q, int seq_k, int n_heads,
+                                     int head_dim, float scale, hipStream_t stream) {
+    return runtime_kv_attn(q, cache_k, cache_v, valid_slots, out, seq_q, seq_k, n_heads, head_dim, INT_MAX, scale,
+                           stream);
+}
+
+int lingbot_runtime_kv_attn_cublas_f32(const float *q, const float *cache_k, const float *cache_v,
+                                       const int *valid_slots, float *out, int seq_q, int seq_k, int n_heads,
+                                       int head_dim, int capacity, float scale, hipStream_t stream) {
+    EMB_CHECK_ARG(capacity > 0, "capacity must be positive");
+    return runtime_kv_attn(q, cache_k, cache_v, valid_slots, out, seq_q, seq_k, n_heads, head_dim, capacity, scale,
+                           stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,295 @@
+"""ctypes binding of libemb_kv.so (the C ABI in include/emb_kv.h).
+
+Device buffers are passed as raw pointers; torch tensors are accepted
+wherever a pointer is expected (their data_ptr() is used), which is how the
+tests and bench.py hold device memory.  Loading fails loudly when the library
+has not been built: there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libemb_kv.so"
+
+_lib = None
+
+EMB_MASK_FULL, EMB_MASK_CHUNK, EMB_MASK_TOKEN, EMB_MASK_ADD, EMB_MASK_BLOCKMAP = range(5)
+
+i32p = C.POINTER(C.c_int32)
+i64p = C.POINTER(C.c_int64)
+u8p = C.POINTER(C.c_uint8)
+u16p = C.POINTER(C.c_uint16)
+vp = C.c_void_p
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [
+        ("q", vp), ("q_is_f32", C.c_int32), ("q_stride", C.c_int64),
+        ("out", vp), ("out_stride", C.c_int64),
+        ("cu_q", vp), ("n_keys", vp), ("q_pos0", vp),
+        ("k_pool", vp), ("v_pool", vp),
+        ("block_tables", vp), ("bt_stride", C.c_int32),
+        ("valid_slots", vp), ("valid_stride", C.c_int32),
+        ("capacity", C.c_int32), ("batch", C.c_int32), ("hq", C.c_int32), ("hkv", C.c_int32),
+        ("head_dim", C.c_int32), ("max_q", C.c_int32), ("scale", C.c_float),
+        ("mask_kind", C.c_int32), ("chunk", C.c_int32), ("window", C.c_int32),
+        ("mask", vp), ("mask_q_stride", C.c_int64), ("mask_batch_stride", C.c_int64),
+        ("block_map", vp), ("block_size", C.c_int32), ("block_map_cols", C.c_int32),
+        ("block_map_batch_stride", C.c_int64),
+        ("splits", C.c_int32), ("workspace", vp),
+    ]
+
+
+_SIGS = {
+    "emb_last_error": (C.c_char_p, []),
+    "emb_version": (C.c_char_p, []),
+    "emb_slot_cache_create": (vp, [C.c_int64, C.c_int]),
+    "emb_slot_cache_destroy": (None, [vp]),
+    "emb_slot_cache_capacity": (C.c_int64, [vp]),
+    "emb_slot_cache_used_count": (C.c_int64, [vp]),
+    "emb_slot_cache_pred_count": (C.c_int64, [vp]),
+    "emb_slot_cache_next_id": (C.c_int64, [vp]),
+    "emb_slot_cache_allocate": (C.c_int, [vp, C.c_int64, i64p]),
+    "emb_slot_cache_update_meta": (C.c_int, [vp, C.c_int64, C.c_int, i64p]),
+    "emb_slot_cache_prepare_mode0": (C.c_int, [vp, C.c_int64, i64p, i64p, i64p]),
+    "emb_slot_cache_restore": (None, [vp, i64p, C.c_int64]),
+    "emb_slot_cache_clear_pred": (None, [vp]),
+    "emb_slot_cache_collect_valid": (C.c_int64, [vp, i64p]),
+    "emb_slot_cache_export": (C.c_int, [vp, i64p, u8p, u8p]),
+    "emb_page_pool_create": (vp, [C.c_int32, C.c_uint64]),
+    "emb_page_pool_destroy": (None, [vp]),
+    "emb_page_pool_free_count": (C.c_int32, [vp]),
+    "emb_slot_cache_bind_pool": (C.c_int, [vp, vp]),
+    "emb_slot_cache_map_range": (C.c_int, [vp, C.c_int64]),
+    "emb_slot_cache_block_table": (C.c_int, [vp, i32p, C.c_int64]),
+    "emb_slot_cache_release_pages": (C.c_int, [vp]),
+    "emb_lingbot_kv_capacity": (C.c_int64, [C.c_int64] * 11),
+    "emb_flex_meta_build": (vp, [C.c_int64] * 16),
+    "emb_flex_meta_destroy": (None, [vp]),
+    "emb_flex_meta_len": (C.c_int64, [vp]),
+    "emb_flex_meta_ids": (C.c_int, [vp, i64p, i64p, i64p]),
+    "emb_flex_self_allowed": (C.c_int, [vp, C.c_int64, C.c_int64]),
+    "emb_flex_cross_allowed": (C.c_int, [vp, C.c_int64, C.c_int64]),
+    "emb_dense_block_table": (C.c_int64, [C.c_int64, C.c_int64, C.c_int64, i32p, i32p]),
+    "emb_self_block_table": (C.c_int64, [vp, i32p, i32p]),
+    "emb_cross_block_table": (C.c_int64, [vp, i32p, i32p]),
+    "emb_self_token_mask": (C.c_int, [vp, u8p]),
+    "emb_kv_append": (C.c_int, [vp, vp, C.c_int64, C.c_int32, vp, vp, C.c_int32, vp, vp,
+                                C.c_int32, C.c_int32, vp]),
+    "emb_kv_gather": (C.c_int, [vp, vp, vp, C.c_int32, vp, C.c_int32, vp, vp, C.c_int32,
+                                C.c_int32, vp]),
+    "emb_attn_workspace_bytes": (C.c_size_t, [C.c_int32] * 6),
+    "emb_paged_attention": (C.c_int, [C.POINTER(AttnArgs), vp]),
+    "lingbot_runtime_kv_update_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int,
+                                                C.c_int, vp]),
+    "lingbot_runtime_kv_gather_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int,
+                                                C.c_int, vp]),
+    "lingbot_runtime_kv_attn_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int,
+                                              C.c_int, C.c_float, vp]),
+    "lingbot_runtime_kv_attn_online_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int,
+                                                     C.c_int, C.c_int, C.c_float, vp]),
+    "lingbot_runtime_kv_attn_warp_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int,
+                                                   C.c_int, C.c_int, C.c_float, vp]),
+    "lingbot_runtime_kv_attn_cublas_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int,
+                                                     C.c_int, C.c_int, C.c_int, C.c_float, vp]),
+    "emb_synth_normal_bf16": (C.c_int, [C.c_uint64, C.c_int64, u16p]),
+}
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/emb_kv.h."""
+    import re
+    text = (PKG.parent / "include" / "emb_kv.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:emb|lingbot|cosmos3)_\w+)\s*\(", text)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().emb_last_error().decode()
+
+
+def check(rc: int, what: str = "") -> int:
+    if rc < 0:
+        raise RuntimeError(f"{what} failed rc={rc}: {last_error()}")
+    return rc
+
+
+def ptr(x) -> int | None:
+    """Device/host pointer of a torch tensor, a numpy array or an int (None -> NULL)."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data
+    raise TypeError(type(x))
+
+
+def stream_ptr(stream=None) -> int | None:
+    if stream is None:
+        return None
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _np_i64(n):
+    a = np.zeros(max(int(n), 1), dtype=np.int64)
+    return a, a.ctypes.data_as(i64p)
+
+
+class SlotCache:
+    """LingBotKVCache semantics (models/lingbot_va.cpp:8740-8997) over libemb_kv."""
+
+    def __init__(self, capacity: int, legacy_clear_pred: bool = False):
+        self.h = lib().emb_slot_cache_create(capacity, int(legacy_clear_pred))
+        if not self.h:
+            raise RuntimeError(last_error())
+        self.capacity = capacity
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.emb_slot_cache_destroy(self.h)
+            self.h = None
+
+    def used_count(self): return lib().emb_slot_cache_used_count(self.h)
+    def pred_count(self): return lib().emb_slot_cache_pred_count(self.h)
+    def next_id(self): return lib().emb_slot_cache_next_id(self.h)
+
+    def allocate(self, key_size):
+        a, p = _np_i64(key_size)
+        rc = lib().emb_slot_cache_allocate(self.h, key_size, p)
+        return (a[:key_size] if rc == 0 else None), rc
+
+    def update_meta(self, key_size, pred):
+        a, p = _np_i64(key_size)
+        rc = lib().emb_slot_cache_update_meta(self.h, key_size, int(pred), p)
+        return (a[:key_size] if rc == 0 else None), rc
+
+    def prepare_mode0(self, key_size):
+        s, sp = _np_i64(key_size)
+        v, vpp = _np_i64(self.capacity)
+        n = C.c_int64(0)
+        rc = lib().emb_slot_cache_prepare_mode0(self.h, key_size, sp, vpp, C.byref(n))
+        if rc != 0:
+            return None, None, rc
+        return s[:key_size], v[: n.value], rc
+
+    def restore(self, slots):
+        a = np.ascontiguousarray(slots, dtype=np.int64)
+        lib().emb_slot_cache_restore(self.h, a.ctypes.data_as(i64p), len(a))
+
+    def clear_pred(self): lib().emb_slot_cache_clear_pred(self.h)
+
+    def collect_valid(self):
+        v, p = _np_i64(self.capacity)
+        n = lib().emb_slot_cache_collect_valid(self.h, p)
+        return v[:n]
+
+    def state(self):
+        idv = np.zeros(self.capacity, np.int64)
+        m = np.zeros(self.capacity, np.uint8)
+        pr = np.zeros(self.capacity, np.uint8)
+        check(lib().emb_slot_cache_export(self.h, idv.ctypes.data_as(i64p), m.ctypes.data_as(u8p),
+                                          pr.ctypes.data_as(u8p)), "export")
+        return idv, m, pr
+
+    def bind_pool(self, pool):
+        check(lib().emb_slot_cache_bind_pool(self.h, pool.h), "bind_pool")
+        self._pool = pool  # the pool must outlive the cache
+    def map_range(self, n): check(lib().emb_slot_cache_map_range(self.h, n), "map_range")
+    def release_pages(self): check(lib().emb_slot_cache_release_pages(self.h), "release_pages")
+
+    def block_table(self, n=None):
+        n = n or (self.capacity + 15) // 16
+        bt = np.zeros(n, np.int32)
+        check(lib().emb_slot_cache_block_table(self.h, bt.ctypes.data_as(i32p), n), "block_table")
+        return bt
+
+
+class PagePool:
+    def __init__(self, n_pages: int, seed: int = 0):
+        self.h = lib().emb_page_pool_create(n_pages, seed)
+        if not self.h:
+            raise RuntimeError(last_error())
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.emb_page_pool_destroy(self.h)
+            self.h = None
+
+    def free_count(self): return lib().emb_page_pool_free_count(self.h)
+
+
+def lingbot_kv_capacity(override_tokens=0, frame_chunk_size=4, action_per_frame=4, n_suffix=0,
+                        attn_window=30, latent_h=8, latent_w=16, patch_t=1, patch_h=2, patch_w=2,
+                        seq=0):
+    return lib().emb_lingbot_kv_capacity(override_tokens, frame_chunk_size, action_per_frame,
+                                         n_suffix, attn_window, latent_h, latent_w, patch_t,
+                                         patch_h, patch_w, seq)
+
+
+def synth_normal_bf16(seed: int, n: int) -> np.ndarray:
+    out = np.zeros(n, np.uint16)
+    check(lib().emb_synth_normal_bf16(seed, n, out.ctypes.data_as(u16p)), "synth")
+    return out
+
+
+def kv_append(k_new, v_new, src_stride, n, slots, block_table, capacity, k_pool, v_pool, hkv, d,
+              stream=None):
+    return check(lib().emb_kv_append(ptr(k_new), ptr(v_new), src_stride, n, ptr(slots),
+                                     ptr(block_table), capacity, ptr(k_pool), ptr(v_pool), hkv, d,
+                                     stream_ptr(stream)), "emb_kv_append")
+
+
+def kv_gather(k_pool, v_pool, valid, n, block_table, capacity, k_out, v_out, hkv, d, stream=None):
+    return check(lib().emb_kv_gather(ptr(k_pool), ptr(v_pool), ptr(valid), n, ptr(block_table),
+                                     capacity, ptr(k_out), ptr(v_out), hkv, d, stream_ptr(stream)),
+                 "emb_kv_gather")
+
+
+def attn_workspace_bytes(batch, max_q, hq, hkv, d, splits):
+    return lib().emb_attn_workspace_bytes(batch, max_q, hq, hkv, d, splits)
+
+
+def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, capacity,
+                    cu_q=None, n_keys=None, q_pos0=None, q_is_f32=False, q_stride=None,
+                    out_stride=None, block_tables=None, bt_stride=0, valid_slots=None,
+                    valid_stride=0, mask_kind=EMB_MASK_FULL, chunk=0, window=-1, mask=None,
+                    mask_q_stride=0, mask_batch_stride=0, block_map=None, block_size=0,
+                    block_map_cols=0, block_map_batch_stride=0, splits=1, workspace=None,
+                    stream=None):
+    a = AttnArgs()
+    a.q = ptr(q); a.q_is_f32 = int(q_is_f32)
+    a.q_stride = q_stride if q_stride is not None else hq * d
+    a.out = ptr(out); a.out_stride = out_stride if out_stride is not None else hq * d
+    a.cu_q = ptr(cu_q); a.n_keys = ptr(n_keys); a.q_pos0 = ptr(q_pos0)
+    a.k_pool = ptr(k_pool); a.v_pool = ptr(v_pool)
+    a.block_tables = ptr(block_tables); a.bt_stride = bt_stride
+    a.valid_slots = ptr(valid_slots); a.valid_stride = valid_stride
+    a.capacity = capacity; a.batch = batch; a.hq = hq; a.hkv = hkv; a.head_dim = d
+    a.max_q = max_q; a.scale = scale
+    a.mask_kind = mask_kind; a.chunk = chunk; a.window = window
+    a.mask = ptr(mask); a.mask_q_stride = mask_q_stride; a.mask_batch_stride = mask_batch_stride
+    a.block_map = ptr(block_map); a.block_size = block_size; a.block_map_cols = block_map_cols
+    a.block_map_batch_stride = block_map_batch_stride
+    a.splits = splits; a.workspace = ptr(workspace)
+    return check(lib().emb_paged_attention(C.byref(a), stream_ptr(stream)), "emb_paged_attention")

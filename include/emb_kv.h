@@ -1,0 +1,236 @@
+/*
+ * emb_kv.h -- C ABI of the MI355X (gfx950) KV-cached attention step.
+ *
+ * One shared library, libemb_kv.so, built from embodied.cpp_amd/csrc/.
+ * Conventions (same as the reference's kernel-level face,
+ * kernels/lingbot/lingbot_flex_attn_cuda.h:9-105 and
+ * kernels/cosmos3/cosmos3_w8_marlin_cuda.h:9-124):
+ *   - every device entry point is asynchronous on the hipStream_t it takes;
+ *   - it returns 0 on success and a negative code otherwise (-1 for bad
+ *     arguments, checked on the host before any launch), and
+ *     emb_last_error() returns a message for the calling thread;
+ *   - all device buffers are owned by the caller; no entry point listed here
+ *     allocates device memory unless its comment says so.
+ *
+ * Page layout of the KV pool (bf16, EMB_PAGE_TOKENS = 16 token slots a page):
+ *   K page p, kv head h, slot row t, dim d : k_pool[((p*H + h)*16 + t)*D + d]
+ *   V page p, kv head h, dim d, slot row t : v_pool[((p*H + h)*D + d)*16 + t]
+ * A sequence's logical slot s lives in page block_table[s / 16], row s % 16;
+ * block_table == NULL means the identity map (page = s / 16).
+ */
+#ifndef EMB_KV_H
+#define EMB_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EMB_PAGE_TOKENS 16
+
+enum {
+    EMB_OK = 0,
+    EMB_ERR_ARG = -1,        /* null pointer / bad size (reference convention) */
+    EMB_ERR_LAUNCH = -2,     /* hipGetLastError after a launch */
+    EMB_ERR_CAPACITY = -3,   /* slot cache / page pool could not satisfy a request */
+    EMB_ERR_UNSUPPORTED = -4 /* shape outside what the kernels are built for */
+};
+
+const char *emb_last_error(void);
+const char *emb_version(void);
+
+/* ============================================================
+ * Host-side slot cache: LingBotKVCache semantics
+ * (models/lingbot_va.cpp:8740-8997), one per (model, session, layer, branch)
+ * key (LingBotRuntimeKVKey, :9066-9089).  Logical slots are backed by pages of
+ * a shared pool once a page pool is bound.
+ * ============================================================ */
+typedef struct emb_slot_cache emb_slot_cache;
+typedef struct emb_page_pool emb_page_pool;
+
+/* LingBotKVCache::init (:8751-8763) for batch 1; legacy_clear_pred plays the
+ * VLA_LINGBOT_RUNTIME_KV_LEGACY_CLEAR_PRED flag (:153-155). */
+emb_slot_cache *emb_slot_cache_create(int64_t capacity, int legacy_clear_pred);
+void emb_slot_cache_destroy(emb_slot_cache *c);
+int64_t emb_slot_cache_capacity(const emb_slot_cache *c);
+int64_t emb_slot_cache_used_count(const emb_slot_cache *c);   /* :8774-8776 */
+int64_t emb_slot_cache_pred_count(const emb_slot_cache *c);   /* :8778-8784 */
+int64_t emb_slot_cache_next_id(const emb_slot_cache *c);      /* :8786-8792 */
+/* allocate_slots_into (:8793-8831): returns 0 and fills slots[key_size]. */
+int emb_slot_cache_allocate(emb_slot_cache *c, int64_t key_size, int64_t *slots);
+/* update_meta_only (:8888-8902): cache modes 1 (pred) and 2 (update). */
+int emb_slot_cache_update_meta(emb_slot_cache *c, int64_t key_size, int pred, int64_t *slots);
+/* prepare_mode0_temp_slots_no_insert (:8904-8944): cache mode 0.
+ * valid must hold capacity entries; *n_valid receives the count. */
+int emb_slot_cache_prepare_mode0(emb_slot_cache *c, int64_t key_size, int64_t *slots,
+                                 int64_t *valid, int64_t *n_valid);
+void emb_slot_cache_restore(emb_slot_cache *c, const int64_t *slots, int64_t n); /* :8946-8952 */
+void emb_slot_cache_clear_pred(emb_slot_cache *c);                                /* :8954-8965 */
+int64_t emb_slot_cache_collect_valid(const emb_slot_cache *c, int64_t *valid);    /* :8967-8972 */
+/* Snapshot of the per-slot metadata (each array has capacity entries). */
+int emb_slot_cache_export(const emb_slot_cache *c, int64_t *id, uint8_t *mask, uint8_t *is_pred);
+
+/* Page pool: host allocator of physical page ids in [0, n_pages).  seed == 0
+ * hands pages out in ascending order, otherwise in a seeded random order. */
+emb_page_pool *emb_page_pool_create(int32_t n_pages, uint64_t seed);
+void emb_page_pool_destroy(emb_page_pool *p);
+int32_t emb_page_pool_free_count(const emb_page_pool *p);
+/* Bind a pool: every slot a later call hands out gets its page mapped. */
+int emb_slot_cache_bind_pool(emb_slot_cache *c, emb_page_pool *p);
+/* Map pages for logical slots [0, n_slots) now (e.g. for a prefix). */
+int emb_slot_cache_map_range(emb_slot_cache *c, int64_t n_slots);
+/* Block table of ceil(capacity/16) entries; unmapped pages are -1. */
+int emb_slot_cache_block_table(const emb_slot_cache *c, int32_t *bt, int64_t n);
+/* Return every mapped page to the pool (session reset). */
+int emb_slot_cache_release_pages(emb_slot_cache *c);
+
+/* lingbot_runtime_kv_capacity (:9217-9249) with the environment lookups made
+ * arguments; override_tokens > 0 plays VLA_LINGBOT_KV_CACHE_TOKENS. */
+int64_t emb_lingbot_kv_capacity(int64_t override_tokens, int64_t frame_chunk_size,
+                                int64_t action_per_frame, int64_t n_suffix,
+                                int64_t attn_window, int64_t latent_h, int64_t latent_w,
+                                int64_t patch_t, int64_t patch_h, int64_t patch_w, int64_t seq);
+
+/* Flex-mask metadata and block tables (models/lingbot_va.cpp:9274-9465). */
+typedef struct emb_flex_meta emb_flex_meta;
+emb_flex_meta *emb_flex_meta_build(int64_t lat_b, int64_t lat_f, int64_t lat_h, int64_t lat_w,
+                                   int64_t act_b, int64_t act_f, int64_t act_h, int64_t act_w,
+                                   int64_t padded_length, int64_t chunk_size,
+                                   int64_t window_size, int64_t pt, int64_t ph, int64_t pw,
+                                   int64_t text_seq, int64_t block_size);
+void emb_flex_meta_destroy(emb_flex_meta *m);
+int64_t emb_flex_meta_len(const emb_flex_meta *m);
+int emb_flex_meta_ids(const emb_flex_meta *m, int64_t *seq_ids, int64_t *frame_ids,
+                      int64_t *noise_ids);
+int emb_flex_self_allowed(const emb_flex_meta *m, int64_t q, int64_t k);  /* :9330-9340 */
+int emb_flex_cross_allowed(const emb_flex_meta *m, int64_t q, int64_t k); /* :9342-9344 */
+/* CSR tables; row_ptr holds q_blocks+1 entries, col_idx q_blocks*kv_blocks.
+ * Return nnz, or a negative error. */
+int64_t emb_dense_block_table(int64_t seq_q, int64_t seq_k, int64_t block_size,
+                              int32_t *row_ptr, int32_t *col_idx);             /* :9354-9372 */
+int64_t emb_self_block_table(const emb_flex_meta *m, int32_t *row_ptr, int32_t *col_idx);
+int64_t emb_cross_block_table(const emb_flex_meta *m, int32_t *row_ptr, int32_t *col_idx);
+int emb_self_token_mask(const emb_flex_meta *m, uint8_t *mask);                /* :9456-9465 */
+
+/* ============================================================
+ * Device data movement (bf16 pool)
+ * ============================================================ */
+
+/* Append n new token rows into the pool: runtime_kv_update (a9,
+ * kernels/lingbot/lingbot_flex_attn_cuda.cu:626-649) made paged.
+ * k_new/v_new: bf16 rows of n_kv_heads*head_dim elements, row stride src_stride
+ * (elements).  slots: int32 [n] logical slots (device); a slot outside
+ * [0, capacity) or on an unmapped page (-1) is skipped, as the reference skips
+ * out-of-range slots. */
+int emb_kv_append(const void *k_new, const void *v_new, int64_t src_stride, int32_t n,
+                  const int32_t *slots, const int32_t *block_table, int32_t capacity,
+                  void *k_pool, void *v_pool, int32_t n_kv_heads, int32_t head_dim,
+                  hipStream_t stream);
+
+/* Gather rows valid[0..n) into compact [n][H][D] bf16 (reference layout):
+ * runtime_kv_gather (a10, :875-898).  Out-of-range slots leave the row as is. */
+int emb_kv_gather(const void *k_pool, const void *v_pool, const int32_t *valid, int32_t n,
+                  const int32_t *block_table, int32_t capacity, void *k_out, void *v_out,
+                  int32_t n_kv_heads, int32_t head_dim, hipStream_t stream);
+
+/* ============================================================
+ * Paged block-masked attention (one launch for a batch of sequences)
+ * ============================================================ */
+enum {
+    EMB_MASK_FULL = 0,    /* every key visible (pi0.5 prefix-LM from the suffix; prefill) */
+    EMB_MASK_CHUNK = 1,   /* chunk-causal: key j visible to query position p iff
+                             j/chunk <= p/chunk and p/chunk - j/chunk <= window
+                             (window < 0: unlimited); chunk = 1 is causal */
+    EMB_MASK_TOKEN = 2,   /* u8 [n_q][n_k] per sequence, 0 = hidden */
+    EMB_MASK_ADD = 3,     /* f32 [n_q][n_k] per sequence added to scaled scores */
+    EMB_MASK_BLOCKMAP = 4 /* u8 block map [q_blocks][k_blocks] (flex CSR) and an
+                             optional u8 token mask */
+};
+
+typedef struct emb_attn_args {
+    /* queries: bf16 (q_is_f32 == 0) or f32, [total_q tokens][hq][d] with token
+     * stride q_stride elements; sequence b owns tokens cu_q[b]..cu_q[b+1]. */
+    const void *q;
+    int32_t q_is_f32;
+    int64_t q_stride;
+    /* output f32 [total_q][hq][d], token stride out_stride elements */
+    float *out;
+    int64_t out_stride;
+    const int32_t *cu_q;       /* device [batch+1] */
+    const int32_t *n_keys;     /* device [batch]: keys per sequence */
+    const int32_t *q_pos0;     /* device [batch] or NULL: position of query 0 in
+                                  key index space (NULL: n_keys - n_q) */
+    /* pool */
+    const void *k_pool, *v_pool;
+    const int32_t *block_tables; /* device [batch][bt_stride] or NULL (identity) */
+    int32_t bt_stride;
+    const int32_t *valid_slots;  /* device [batch][valid_stride] or NULL: key j is
+                                    logical slot j; else key j is slot valid[j]
+                                    (a negative entry is a zero K/V row, the
+                                    online-kernel behaviour of :722-792) */
+    int32_t valid_stride;
+    int32_t capacity;            /* logical slots per sequence (bounds check) */
+    int32_t batch, hq, hkv, head_dim;
+    int32_t max_q;               /* max query tokens over the batch (host) */
+    float scale;
+    /* mask */
+    int32_t mask_kind;
+    int32_t chunk, window;             /* EMB_MASK_CHUNK */
+    const void *mask;                  /* TOKEN: u8, ADD: f32 */
+    int64_t mask_q_stride;             /* elements between query rows */
+    int64_t mask_batch_stride;         /* elements between sequences */
+    const uint8_t *block_map;          /* BLOCKMAP: [q_blocks][k_blocks] per sequence */
+    int32_t block_size, block_map_cols;
+    int64_t block_map_batch_stride;
+    /* split-K over keys: 0/1 = none.  With splits > 1, workspace must hold
+     * emb_attn_workspace_bytes(...) bytes of device memory. */
+    int32_t splits;
+    void *workspace;
+} emb_attn_args;
+
+size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_t hkv,
+                                int32_t head_dim, int32_t splits);
+int emb_paged_attention(const emb_attn_args *a, hipStream_t stream);
+
+/* ============================================================
+ * Reference-named kernel-level face (same signatures as
+ * kernels/lingbot/lingbot_flex_attn_cuda.h:13-105 with hipStream_t).
+ * cache_k/cache_v are device buffers the caller sized for the reference's f32
+ * cache (capacity*n_heads*head_dim floats); this library keeps them as a bf16
+ * identity-paged pool inside that space, which needs capacity >= 8.  f32
+ * inputs are rounded to bf16 (round to nearest even) on append.
+ * ============================================================ */
+int lingbot_runtime_kv_update_f32(const float *k, const float *v, float *cache_k, float *cache_v,
+                                  const int *slots, int seq, int n_heads, int head_dim,
+                                  int capacity, hipStream_t stream);
+int lingbot_runtime_kv_gather_f32(const float *cache_k, const float *cache_v,
+                                  const int *valid_slots, float *compact_k, float *compact_v,
+                                  int seq_k, int n_heads, int head_dim, int capacity,
+                                  hipStream_t stream);
+int lingbot_runtime_kv_attn_f32(const float *q, const float *cache_k, const float *cache_v,
+                                const int *valid_slots, float *out, int seq_q, int seq_k,
+                                int n_heads, int head_dim, float scale, hipStream_t stream);
+int lingbot_runtime_kv_attn_online_f32(const float *q, const float *cache_k,
+                                       const float *cache_v, const int *valid_slots, float *out,
+                                       int seq_q, int seq_k, int n_heads, int head_dim,
+                                       float scale, hipStream_t stream);
+int lingbot_runtime_kv_attn_warp_f32(const float *q, const float *cache_k, const float *cache_v,
+                                     const int *valid_slots, float *out, int seq_q, int seq_k,
+                                     int n_heads, int head_dim, float scale, hipStream_t stream);
+/* Called at models/lingbot_va.cpp:9622 but defined nowhere in the reference. */
+int lingbot_runtime_kv_attn_cublas_f32(const float *q, const float *cache_k,
+                                       const float *cache_v, const int *valid_slots, float *out,
+                                       int seq_q, int seq_k, int n_heads, int head_dim,
+                                       int capacity, float scale, hipStream_t stream);
+
+/* Synthetic inputs for the bench: N(0,1) bf16 from std::mt19937_64(seed)
+ * (Box-Muller on 53-bit uniforms), written to host memory. */
+int emb_synth_normal_bf16(uint64_t seed, int64_t n, uint16_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,322 @@
+"""Python binding of the CPU oracle (oracle/build/libemb_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU baseline,
+never by the product library.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "build" / "libemb_oracle.so"
+
+i32p = C.POINTER(C.c_int32)
+i64p = C.POINTER(C.c_int64)
+u8p = C.POINTER(C.c_uint8)
+i8p = C.POINTER(C.c_int8)
+u16p = C.POINTER(C.c_uint16)
+f32p = C.POINTER(C.c_float)
+vp = C.c_void_p
+
+_SIGS = {
+    "orc_bf16_to_f32": (C.c_float, [C.c_uint16]),
+    "orc_f32_to_bf16": (C.c_uint16, [C.c_float]),
+    "orc_fill_normal_bf16": (None, [C.c_uint64, C.c_int64, u16p]),
+    "orc_mt64_nth": (C.c_uint64, [C.c_uint64, C.c_int64]),
+    "orc_cache_new": (vp, [C.c_int64, C.c_int]),
+    "orc_cache_free": (None, [vp]),
+    "orc_cache_used_count": (C.c_int64, [vp]),
+    "orc_cache_pred_count": (C.c_int64, [vp]),
+    "orc_cache_next_id": (C.c_int64, [vp]),
+    "orc_cache_allocate": (C.c_int, [vp, C.c_int64, i64p]),
+    "orc_cache_update_meta": (C.c_int, [vp, C.c_int64, C.c_int, i64p]),
+    "orc_cache_prepare_mode0": (C.c_int, [vp, C.c_int64, i64p, i64p, i64p]),
+    "orc_cache_restore": (None, [vp, i64p, C.c_int64]),
+    "orc_cache_clear_pred": (None, [vp]),
+    "orc_cache_collect_valid": (C.c_int64, [vp, i64p]),
+    "orc_cache_id_ptr": (i64p, [vp]),
+    "orc_cache_mask_ptr": (u8p, [vp]),
+    "orc_cache_is_pred_ptr": (u8p, [vp]),
+    "orc_lingbot_capacity": (C.c_int64, [C.c_int64] * 11),
+    "orc_slot_update": (None, [u16p, u16p, u16p, u16p, i32p, C.c_int64, C.c_int64, C.c_int64,
+                               C.c_int64]),
+    "orc_slot_gather": (None, [u16p, u16p, i32p, u16p, u16p, C.c_int64, C.c_int64, C.c_int64,
+                               C.c_int64]),
+    "orc_paged_append": (None, [u16p, u16p, C.c_int64, C.c_int64, C.c_int64, C.c_int64, i32p,
+                                i32p, C.c_int64, u16p, u16p]),
+    "orc_paged_gather": (None, [u16p, u16p, i32p, C.c_int64, C.c_int64, C.c_int64, i32p,
+                                C.c_int64, u16p, u16p]),
+    "orc_flex_meta_build": (vp, [C.c_int64] * 16),
+    "orc_flex_meta_free": (None, [vp]),
+    "orc_flex_self_allowed": (C.c_int, [vp, C.c_int64, C.c_int64]),
+    "orc_flex_cross_allowed": (C.c_int, [vp, C.c_int64, C.c_int64]),
+    "orc_dense_block_table": (C.c_int64, [C.c_int64, C.c_int64, C.c_int64, i64p, i64p]),
+    "orc_self_block_table": (C.c_int64, [vp, i64p, i64p]),
+    "orc_cross_block_table": (C.c_int64, [vp, i64p, i64p]),
+    "orc_self_token_mask": (None, [vp, u8p]),
+    "orc_max_row_nnz": (C.c_int64, [i64p, C.c_int64]),
+    "orc_dense_masked_attention": (None, [f32p, f32p, f32p, u8p, C.c_int64, C.c_int64, C.c_int64,
+                                          f32p]),
+    "orc_flex_attention": (None, [f32p, f32p, f32p, i32p, i32p, u8p, f32p, C.c_int64, C.c_int64,
+                                  C.c_int64, C.c_int64, C.c_int64, C.c_float]),
+    "orc_runtime_kv_attn": (None, [f32p, f32p, f32p, i32p, f32p, C.c_int64, C.c_int64, C.c_int64,
+                                   C.c_int64, C.c_float, C.c_int]),
+    "orc_gqa_attention_bf16": (None, [u16p, u16p, u16p, C.c_int64, C.c_int64, C.c_int64,
+                                      C.c_int64, C.c_int64, C.c_float, u8p, f32p, C.c_int64,
+                                      C.c_int64, C.c_int64, i64p, C.c_int64, C.c_int, f32p]),
+    "orc_marlin_dst_byte": (C.c_int64, [C.c_int64, C.c_int64, C.c_int64]),
+    "orc_marlin_scale_index": (C.c_int64, [C.c_int64]),
+    "orc_marlin_pack_w8": (None, [i8p, C.c_int64, C.c_int64, i32p]),
+    "orc_marlin_unpack_w8": (C.c_int, [i32p, C.c_int64, C.c_int64, C.c_int64, C.c_int64]),
+    "orc_marlin_pack_scales": (None, [u16p, C.c_int64, u16p]),
+    "orc_w8a16_gemm": (None, [u16p, i32p, u16p, C.c_int64, C.c_int64, C.c_int64, i64p, C.c_int64,
+                              C.c_int, u16p, f32p]),
+}
+
+_lib = None
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} missing; run `make -C oracle`")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def P(a: np.ndarray, t):
+    return None if a is None else a.ctypes.data_as(t)
+
+
+# ---------------- bf16 helpers (numpy, vectorised, RNE) ----------------
+def bf16_to_f32(u16: np.ndarray) -> np.ndarray:
+    return (u16.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(f: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(f, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(np.asarray(f, np.float32))
+    if nan.any():
+        r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def normal_bf16(seed: int, n: int) -> np.ndarray:
+    out = np.zeros(n, np.uint16)
+    lib().orc_fill_normal_bf16(seed, n, P(out, u16p))
+    return out
+
+
+# ---------------- slot cache ----------------
+class Cache:
+    def __init__(self, total, legacy=False):
+        self.h = lib().orc_cache_new(total, int(legacy))
+        self.total = total
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.orc_cache_free(self.h)
+            self.h = None
+
+    def used_count(self): return lib().orc_cache_used_count(self.h)
+    def pred_count(self): return lib().orc_cache_pred_count(self.h)
+    def next_id(self): return lib().orc_cache_next_id(self.h)
+
+    def allocate(self, k):
+        a = np.zeros(max(k, 1), np.int64)
+        ok = lib().orc_cache_allocate(self.h, k, P(a, i64p))
+        return a[:k] if ok else None
+
+    def update_meta(self, k, pred):
+        a = np.zeros(max(k, 1), np.int64)
+        ok = lib().orc_cache_update_meta(self.h, k, int(pred), P(a, i64p))
+        return a[:k] if ok else None
+
+    def prepare_mode0(self, k):
+        s = np.zeros(max(k, 1), np.int64)
+        v = np.zeros(self.total, np.int64)
+        n = C.c_int64(0)
+        ok = lib().orc_cache_prepare_mode0(self.h, k, P(s, i64p), P(v, i64p), C.byref(n))
+        return (s[:k], v[: n.value]) if ok else (None, None)
+
+    def restore(self, slots):
+        a = np.ascontiguousarray(slots, np.int64)
+        lib().orc_cache_restore(self.h, P(a, i64p), len(a))
+
+    def clear_pred(self): lib().orc_cache_clear_pred(self.h)
+
+    def collect_valid(self):
+        v = np.zeros(self.total, np.int64)
+        n = lib().orc_cache_collect_valid(self.h, P(v, i64p))
+        return v[:n]
+
+    def state(self):
+        L = lib()
+        ids = np.ctypeslib.as_array(L.orc_cache_id_ptr(self.h), (self.total,)).copy()
+        m = np.ctypeslib.as_array(L.orc_cache_mask_ptr(self.h), (self.total,)).copy()
+        pr = np.ctypeslib.as_array(L.orc_cache_is_pred_ptr(self.h), (self.total,)).copy()
+        return ids, m, pr
+
+
+def lingbot_capacity(override_tokens=0, frame_chunk_size=4, action_per_frame=4, n_suffix=0,
+                     attn_window=30, latent_h=8, latent_w=16, patch_t=1, patch_h=2, patch_w=2,
+                     seq=0):
+    return lib().orc_lingbot_capacity(override_tokens, frame_chunk_size, action_per_frame,
+                                      n_suffix, attn_window, latent_h, latent_w, patch_t, patch_h,
+                                      patch_w, seq)
+
+
+# ---------------- movement ----------------
+def slot_update(k, v, cache_k, cache_v, slots, heads, d, capacity):
+    s = np.ascontiguousarray(slots, np.int32)
+    lib().orc_slot_update(P(k, u16p), P(v, u16p), P(cache_k, u16p), P(cache_v, u16p), P(s, i32p),
+                          len(s), heads, d, capacity)
+
+
+def slot_gather(cache_k, cache_v, valid, heads, d, capacity, out_k, out_v):
+    s = np.ascontiguousarray(valid, np.int32)
+    lib().orc_slot_gather(P(cache_k, u16p), P(cache_v, u16p), P(s, i32p), P(out_k, u16p),
+                          P(out_v, u16p), len(s), heads, d, capacity)
+
+
+def paged_append(k, v, src_stride, slots, block_table, heads, d, capacity, k_pool, v_pool):
+    s = np.ascontiguousarray(slots, np.int32)
+    bt = None if block_table is None else np.ascontiguousarray(block_table, np.int32)
+    lib().orc_paged_append(P(k, u16p), P(v, u16p), src_stride, len(s), heads, d, P(s, i32p),
+                           P(bt, i32p), capacity, P(k_pool, u16p), P(v_pool, u16p))
+
+
+def paged_gather(k_pool, v_pool, valid, block_table, heads, d, capacity, k_out, v_out):
+    s = np.ascontiguousarray(valid, np.int32)
+    bt = None if block_table is None else np.ascontiguousarray(block_table, np.int32)
+    lib().orc_paged_gather(P(k_pool, u16p), P(v_pool, u16p), P(s, i32p), len(s), heads, d,
+                           P(bt, i32p), capacity, P(k_out, u16p), P(v_out, u16p))
+
+
+# ---------------- flex ----------------
+class FlexMeta:
+    def __init__(self, *args):
+        self.h = lib().orc_flex_meta_build(*args)
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.orc_flex_meta_free(self.h)
+            self.h = None
+
+
+def self_block_table(meta, n, bs):
+    qb = (n + bs - 1) // bs
+    rp = np.zeros(qb + 1, np.int64)
+    ci = np.zeros(max(qb * qb, 1), np.int64)
+    nnz = lib().orc_self_block_table(meta.h, P(rp, i64p), P(ci, i64p))
+    return rp, ci[:nnz]
+
+
+def cross_block_table(meta, n, n_text, bs):
+    qb, kb = (n + bs - 1) // bs, (n_text + bs - 1) // bs
+    rp = np.zeros(qb + 1, np.int64)
+    ci = np.zeros(max(qb * kb, 1), np.int64)
+    nnz = lib().orc_cross_block_table(meta.h, P(rp, i64p), P(ci, i64p))
+    return rp, ci[:nnz]
+
+
+def dense_block_table(sq, sk, bs):
+    qb, kb = (sq + bs - 1) // bs, (sk + bs - 1) // bs
+    rp = np.zeros(qb + 1, np.int64)
+    ci = np.zeros(max(qb * kb, 1), np.int64)
+    nnz = lib().orc_dense_block_table(sq, sk, bs, P(rp, i64p), P(ci, i64p))
+    return rp, ci[:nnz]
+
+
+def self_token_mask(meta, n):
+    m = np.zeros(n * n, np.uint8)
+    lib().orc_self_token_mask(meta.h, P(m, u8p))
+    return m.reshape(n, n)
+
+
+# ---------------- attention ----------------
+def dense_masked_attention(q, k, v, mask, seq, heads, d):
+    out = np.zeros(seq * heads * d, np.float32)
+    lib().orc_dense_masked_attention(P(q, f32p), P(k, f32p), P(v, f32p), P(mask, u8p), seq, heads,
+                                     d, P(out, f32p))
+    return out
+
+
+def flex_attention(q, k, v, row_ptr, col_idx, token_mask, sq, sk, heads, d, bs, scale):
+    out = np.zeros(sq * heads * d, np.float32)
+    rp = np.ascontiguousarray(row_ptr, np.int32)
+    ci = np.ascontiguousarray(col_idx, np.int32)
+    tm = None if token_mask is None else np.ascontiguousarray(token_mask, np.uint8)
+    lib().orc_flex_attention(P(q, f32p), P(k, f32p), P(v, f32p), P(rp, i32p), P(ci, i32p),
+                             P(tm, u8p), P(out, f32p), sq, sk, heads, d, bs, scale)
+    return out
+
+
+def runtime_kv_attn(q, cache_k, cache_v, valid, sq, heads, d, scale, online_quirk=True):
+    vs = np.ascontiguousarray(valid, np.int32)
+    out = np.zeros(sq * heads * d, np.float32)
+    lib().orc_runtime_kv_attn(P(q, f32p), P(cache_k, f32p), P(cache_v, f32p), P(vs, i32p),
+                              P(out, f32p), sq, len(vs), heads, d, scale, int(online_quirk))
+    return out
+
+
+def gqa_attention(q, k, v, n_q, n_k, hq, hkv, d, scale, allow=None, add=None, chunk=0,
+                  window=-1, q_pos0=None, rows=None, threads=0):
+    """q/k/v: uint16 bf16 bits ([n_q][hq][d], [n_k][hkv][d]); returns f32 [n_q][hq][d]
+    (rows not evaluated are zero)."""
+    out = np.zeros(n_q * hq * d, np.float32)
+    if q_pos0 is None:
+        q_pos0 = n_k - n_q
+    r = None if rows is None else np.ascontiguousarray(rows, np.int64)
+    al = None if allow is None else np.ascontiguousarray(allow, np.uint8)
+    ad = None if add is None else np.ascontiguousarray(add, np.float32)
+    lib().orc_gqa_attention_bf16(P(q, u16p), P(k, u16p), P(v, u16p), n_q, n_k, hq, hkv, d, scale,
+                                 P(al, u8p), P(ad, f32p), chunk, window, q_pos0, P(r, i64p),
+                                 0 if r is None else len(r), threads, P(out, f32p))
+    return out.reshape(n_q, hq, d)
+
+
+# ---------------- W8 ----------------
+def marlin_pack_w8(w: np.ndarray) -> np.ndarray:
+    K, N = w.shape
+    q = np.zeros((K // 16, 4 * N), np.int32)
+    lib().orc_marlin_pack_w8(P(np.ascontiguousarray(w, np.int8), i8p), K, N, P(q, i32p))
+    return q
+
+
+def marlin_unpack_w8(q, K, N, k, n):
+    return lib().orc_marlin_unpack_w8(P(q, i32p), K, N, k, n)
+
+
+def marlin_pack_scales(s: np.ndarray) -> np.ndarray:
+    out = np.zeros_like(s, dtype=np.uint16)
+    lib().orc_marlin_pack_scales(P(np.ascontiguousarray(s, np.uint16), u16p), len(s),
+                                 P(out, u16p))
+    return out
+
+
+def w8a16_gemm(x, qweight, s_stored, M, K, N, rows=None, threads=0):
+    r = None if rows is None else np.ascontiguousarray(rows, np.int64)
+    nr = M if r is None else len(r)
+    yb = np.zeros(nr * N, np.uint16)
+    yf = np.zeros(nr * N, np.float32)
+    lib().orc_w8a16_gemm(P(x, u16p), P(qweight, i32p), P(s_stored, u16p), M, K, N, P(r, i64p),
+                         nr, threads, P(yb, u16p), P(yf, f32p))
+    return yb.reshape(nr, N), yf.reshape(nr, N)

@@ -1,0 +1,49 @@
+"""Shared test setup: markers, library handles and comparison helpers."""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+for p in (ROOT / "embodied.cpp_amd", ROOT / "oracle"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+# Tolerances for floating-point outputs.
+MAX_ABS = 2e-2
+MEAN_REL = 1e-3
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (run with -m gpu)")
+
+
+@pytest.fixture(scope="session")
+def orc():
+    import oracle
+    return oracle
+
+
+@pytest.fixture(scope="session")
+def emb():
+    import embkv
+    embkv.lib()
+    return embkv
+
+
+def rel_err(a: np.ndarray, b: np.ndarray) -> tuple[float, float]:
+    """(max |a-b|, sum|a-b| / sum|b|) -- mean-rel is the relative L1 error."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    d = np.abs(a - b)
+    return float(d.max(initial=0.0)), float(d.sum() / max(np.abs(b).sum(), 1e-30))
+
+
+def assert_close(a, b, what="", max_abs=MAX_ABS, mean_rel=MEAN_REL):
+    assert np.all(np.isfinite(a)), f"{what}: non-finite output"
+    mx, mr = rel_err(a, b)
+    assert mx <= max_abs and mr <= mean_rel, f"{what}: max_abs={mx:.3e} mean_rel={mr:.3e}"
+    return mx, mr

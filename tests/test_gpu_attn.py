@@ -1,0 +1,272 @@
+"""GPU parity of the paged block-masked attention against the oracle.
+
+Bar: max |gpu - oracle| <= 2e-2 and sum|gpu - oracle| / sum|oracle| <= 1e-3 on
+identical seeded bf16 inputs.  The pool is built
+on the host by the oracle's paged append, so these tests isolate the
+attention kernel from the append kernel.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return torch, torch.device("cuda")
+
+
+def _t(torch, dev, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to(dev)
+
+
+def _bf16(orc, rng, shape):
+    return orc.f32_to_bf16(rng.standard_normal(shape).astype(np.float32))
+
+
+class Seqs:
+    """A batch of sequences whose keys live in one shared, randomly permuted page pool."""
+
+    def __init__(self, orc, rng, n_keys, n_q, hq, hkv, d, extra_pages=5):
+        self.n_keys, self.n_q = list(n_keys), list(n_q)
+        self.hq, self.hkv, self.d = hq, hkv, d
+        pages = [(k + 15) // 16 for k in n_keys]
+        self.bt_stride = max(pages)
+        total = sum(pages) + extra_pages
+        perm = rng.permutation(total).astype(np.int32)
+        self.bt = np.full((len(n_keys), self.bt_stride), -1, np.int32)
+        o = 0
+        for b, p in enumerate(pages):
+            self.bt[b, :p] = perm[o:o + p]
+            o += p
+        self.k = [_bf16(orc, rng, (k, hkv, d)) for k in n_keys]
+        self.v = [_bf16(orc, rng, (k, hkv, d)) for k in n_keys]
+        self.q = [_bf16(orc, rng, (q, hq, d)) for q in n_q]
+        self.kp = rng.integers(0, 65536, total * hkv * 16 * d, dtype=np.uint16)  # garbage elsewhere
+        self.vp = rng.integers(0, 65536, total * hkv * 16 * d, dtype=np.uint16)
+        # keep garbage finite-free of NaN/Inf so a stray read would show as error, not NaN
+        for a in (self.kp, self.vp):
+            a &= np.uint16(0xBFFF)
+        self.cap = self.bt_stride * 16
+        for b, k in enumerate(n_keys):
+            orc.paged_append(self.k[b], self.v[b], hkv * d, np.arange(k, dtype=np.int32), self.bt[b],
+                             hkv, d, self.cap, self.kp, self.vp)
+        self.cu_q = np.concatenate([[0], np.cumsum(n_q)]).astype(np.int32)
+
+    def run(self, emb, torch, dev, scale, splits=1, **kw):
+        out = torch.full((int(self.cu_q[-1]), self.hq, self.d), float("nan"), dtype=torch.float32, device=dev)
+        ws = None
+        if splits > 1:
+            nb = emb.attn_workspace_bytes(len(self.n_q), max(self.n_q), self.hq, self.hkv, self.d, splits)
+            ws = torch.empty(nb // 4 + 4, dtype=torch.float32, device=dev)
+        keep = dict(q=_t(torch, dev, np.concatenate(self.q)), kp=_t(torch, dev, self.kp),
+                    vp=_t(torch, dev, self.vp), bt=_t(torch, dev, self.bt), cu=_t(torch, dev, self.cu_q),
+                    nk=_t(torch, dev, np.array(self.n_keys, np.int32)))
+        emb.paged_attention(q=keep["q"], out=out, k_pool=keep["kp"], v_pool=keep["vp"], batch=len(self.n_q),
+                            hq=self.hq, hkv=self.hkv, d=self.d, max_q=max(self.n_q), scale=scale,
+                            capacity=self.cap, cu_q=keep["cu"], n_keys=keep["nk"], block_tables=keep["bt"],
+                            bt_stride=self.bt_stride, splits=splits, workspace=ws, **kw)
+        torch.cuda.synchronize()
+        o = out.cpu().numpy()
+        return [o[self.cu_q[b]:self.cu_q[b + 1]] for b in range(len(self.n_q))]
+
+    def oracle(self, orc, b, scale, rows=None, **kw):
+        return orc.gqa_attention(self.q[b], self.k[b], self.v[b], self.n_q[b], self.n_keys[b], self.hq, self.hkv,
+                                 self.d, scale, rows=rows, **kw)
+
+
+def test_pi05_action_expert_shape(emb, orc, torch_dev):
+    """cfg1: prefix 816 + 51 new keys, 51 queries x 8 heads over 1 kv head, D=256, all visible."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0000)
+    s = Seqs(orc, rng, [867], [51], 8, 1, 256)
+    scale = 1 / 16
+    got = s.run(emb, torch, dev, scale)[0]
+    assert_close(got, s.oracle(orc, 0, scale), "pi05 cfg1")
+    got4 = s.run(emb, torch, dev, scale, splits=4)[0]
+    assert_close(got4, s.oracle(orc, 0, scale), "pi05 cfg1 split-K 4")
+
+
+def test_multi_session_sweep(emb, orc, torch_dev):
+    """cfg4: sessions with prefix lengths U[300,1200] + 51 queries, pages scattered in one pool."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0004)
+    L = rng.integers(300, 1201, 8)
+    s = Seqs(orc, rng, [int(x) + 51 for x in L], [51] * 8, 8, 1, 256)
+    got = s.run(emb, torch, dev, 1 / 16)
+    for b in range(8):
+        assert_close(got[b], s.oracle(orc, b, 1 / 16), f"session {b}")
+
+
+def test_prefill_prefix_lm_rows(emb, orc, torch_dev):
+    """cfg2: 816-token bidirectional prefix prefill, 8 q heads / 1 kv head, D=256 (row sample)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0001)
+    s = Seqs(orc, rng, [816], [816], 8, 1, 256)
+    got = s.run(emb, torch, dev, 1 / 16)[0]
+    rows = np.concatenate([np.arange(0, 20), np.arange(400, 420), np.arange(796, 816)])
+    ref = s.oracle(orc, 0, 1 / 16, rows=rows)
+    assert_close(got[rows], ref[rows], "prefill rows")
+
+
+def test_lingbot_chunk_step_rows(emb, orc, torch_dev):
+    """cfg3: 1560 queries x 24 heads (MHA) over 8 prior chunks + the current one (14040 keys), D=128."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0002)
+    s = Seqs(orc, rng, [14040], [1560], 24, 24, 128)
+    got = s.run(emb, torch, dev, 1 / math.sqrt(128))[0]
+    rows = np.array([0, 1, 31, 32, 777, 1023, 1500, 1559])
+    ref = s.oracle(orc, 0, 1 / math.sqrt(128), rows=rows)
+    assert_close(got[rows], ref[rows], "lingbot rows")
+
+
+@pytest.mark.parametrize("window", [-1, 1])
+def test_chunk_causal_prefill(emb, orc, torch_dev, window):
+    """Multi-chunk prefill under the chunk-causal mask (bidirectional inside a chunk)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(5 + window)
+    s = Seqs(orc, rng, [390], [390], 4, 4, 128)
+    got = s.run(emb, torch, dev, 0.09, mask_kind=emb.EMB_MASK_CHUNK, chunk=130, window=window)[0]
+    ref = s.oracle(orc, 0, 0.09, chunk=130, window=window)
+    assert_close(got, ref, f"chunk-causal window={window}")
+
+
+def test_token_mask_hy_vla_suffix(emb, orc, torch_dev):
+    """HY-VLA expert mask (models/hy_vla.cpp:2831-2843): every row sees the prefix;
+    suffix row 0 (state) sees only itself among the suffix."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(9)
+    n_pref, n_suf = 100, 51
+    s = Seqs(orc, rng, [n_pref + n_suf], [n_suf], 8, 2, 128)
+    allow = np.ones((n_suf, n_pref + n_suf), np.uint8)
+    allow[0, n_pref + 1:] = 0
+    m = _t(*torch_dev, allow)
+    got = s.run(emb, torch, dev, 0.088, mask_kind=emb.EMB_MASK_TOKEN, mask=m,
+                mask_q_stride=n_pref + n_suf)[0]
+    assert_close(got, s.oracle(orc, 0, 0.088, allow=allow), "hy_vla token mask")
+
+
+def test_additive_mask(emb, orc, torch_dev):
+    """ggml soft_max_ext / flash_attn_ext additive mask, with -inf entries and an empty row."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(10)
+    nq, nk = 37, 200
+    s = Seqs(orc, rng, [nk], [nq], 8, 1, 64)
+    add = rng.standard_normal((nq, nk)).astype(np.float32)
+    add[rng.random((nq, nk)) < 0.3] = -np.inf
+    add[5] = -np.inf
+    got = s.run(emb, torch, dev, 0.125, mask_kind=emb.EMB_MASK_ADD, mask=_t(torch, dev, add),
+                mask_q_stride=nk)[0]
+    ref = s.oracle(orc, 0, 0.125, add=add)
+    assert np.all(got[5] == 0)
+    assert_close(got, ref, "additive mask")
+
+
+def test_flex_block_map_and_token_mask(emb, orc, torch_dev):
+    """Flex attention (lingbot_flex_attn_cuda.cu:502-582): CSR block table as a block map plus the
+    LingBot chunk-causal token mask from build_flex_mask_meta."""
+    torch, dev = torch_dev
+    meta = orc.FlexMeta(1, 4, 4, 4, 1, 4, 2, 1, 3, 2, 1, 2, 2, 2, 7, 8)
+    # meta length: 2*latent + 2*action + pad = 2*(2*2*2) + 2*(4*2*1) + 3 = 35
+    n = 35
+    tm = orc.self_token_mask(meta, n)
+    bs = 8
+    rp, ci = orc.self_block_table(meta, n, bs)
+    qb = (n + bs - 1) // bs
+    bmap = np.zeros((qb, qb), np.uint8)
+    for r in range(qb):
+        bmap[r, ci[rp[r]:rp[r + 1]]] = 1
+    rng = np.random.default_rng(12)
+    H, D = 2, 64
+    s = Seqs(orc, rng, [n], [n], H, H, D)
+    got = s.run(emb, torch, dev, 0.125, mask_kind=emb.EMB_MASK_BLOCKMAP, block_map=_t(torch, dev, bmap),
+                block_size=bs, block_map_cols=qb, mask=_t(torch, dev, tm), mask_q_stride=n)[0]
+    qf, kf, vf = (orc.bf16_to_f32(x).reshape(-1) for x in (s.q[0], s.k[0], s.v[0]))
+    ref = orc.flex_attention(qf, kf, vf, rp, ci, tm, n, n, H, D, bs, 0.125).reshape(n, H, D)
+    assert_close(got, ref, "flex block map")
+
+
+def test_valid_slot_list_with_gaps_and_negative_slots(emb, orc, torch_dev):
+    """runtime_kv_attn over an arbitrary valid-slot list (LingBot after eviction and mode 0):
+    a negative slot is a zero K/V row, as in the online/warp reference kernels."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(13)
+    H, D, cap, nq = 4, 128, 300, 33
+    ck = _bf16(orc, rng, (cap, H, D))
+    cv = _bf16(orc, rng, (cap, H, D))
+    q = _bf16(orc, rng, (nq, H, D))
+    valid = np.concatenate([np.arange(16, 48), rng.choice(np.arange(48, cap), 150, replace=False), [-1, -1],
+                            np.arange(0, 7)]).astype(np.int32)
+    n_pages = cap // 16 + 1
+    bt = rng.permutation(n_pages + 2)[:n_pages].astype(np.int32)
+    kp = np.zeros((n_pages + 2) * H * 16 * D, np.uint16)
+    vp = np.zeros_like(kp)
+    orc.paged_append(ck, cv, H * D, np.arange(cap, dtype=np.int32), bt, H, D, cap, kp, vp)
+    out = torch.zeros((nq, H, D), dtype=torch.float32, device=dev)
+    keep = [_t(torch, dev, x) for x in (q, kp, vp, bt, valid)]
+    emb.paged_attention(q=keep[0], out=out, k_pool=keep[1], v_pool=keep[2], batch=1, hq=H, hkv=H, d=D,
+                        max_q=nq, scale=0.1, capacity=cap, cu_q=_t(torch, dev, np.array([0, nq], np.int32)),
+                        n_keys=_t(torch, dev, np.array([len(valid)], np.int32)), block_tables=keep[3],
+                        bt_stride=n_pages, valid_slots=keep[4], valid_stride=len(valid))
+    torch.cuda.synchronize()
+    ref = orc.runtime_kv_attn(orc.bf16_to_f32(q).reshape(-1), orc.bf16_to_f32(ck).reshape(-1),
+                              orc.bf16_to_f32(cv).reshape(-1), valid, nq, H, D, 0.1).reshape(nq, H, D)
+    assert_close(out.cpu().numpy(), ref, "valid list")
+
+
+def test_reference_named_runtime_kv_attention(emb, orc, torch_dev):
+    """lingbot_runtime_kv_{update,attn,attn_online,attn_warp,attn_cublas}_f32 with the
+    reference's signatures (kernels/lingbot/lingbot_flex_attn_cuda.h:46-93)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(14)
+    H, D, cap, nq = 3, 128, 96, 20
+    kb, vb, qb = _bf16(orc, rng, (cap, H, D)), _bf16(orc, rng, (cap, H, D)), _bf16(orc, rng, (nq, H, D))
+    kf, vf, qf = orc.bf16_to_f32(kb), orc.bf16_to_f32(vb), orc.bf16_to_f32(qb)
+    ck = torch.zeros(cap * H * D, dtype=torch.float32, device=dev)
+    cv = torch.zeros_like(ck)
+    L = emb.lib()
+    tk, tv, tq = _t(torch, dev, kf), _t(torch, dev, vf), _t(torch, dev, qf)
+    slots = _t(torch, dev, np.arange(cap, dtype=np.int32))
+    assert L.lingbot_runtime_kv_update_f32(tk.data_ptr(), tv.data_ptr(), ck.data_ptr(), cv.data_ptr(),
+                                           slots.data_ptr(), cap, H, D, cap, None) == 0
+    valid = np.array(list(range(0, 40)) + list(range(50, 96)), np.int32)
+    tvld = _t(torch, dev, valid)
+    ref = orc.runtime_kv_attn(qf.reshape(-1), kf.reshape(-1), vf.reshape(-1), valid, nq, H, D,
+                              1 / math.sqrt(D)).reshape(nq, H, D)
+    for name in ("lingbot_runtime_kv_attn_f32", "lingbot_runtime_kv_attn_online_f32",
+                 "lingbot_runtime_kv_attn_warp_f32", "lingbot_runtime_kv_attn_cublas_f32"):
+        out = torch.zeros((nq, H, D), dtype=torch.float32, device=dev)
+        args = [tq.data_ptr(), ck.data_ptr(), cv.data_ptr(), tvld.data_ptr(), out.data_ptr(), nq, len(valid), H, D]
+        if name.endswith("cublas_f32"):
+            args.append(cap)
+        rc = getattr(L, name)(*args, 1 / math.sqrt(D), None)
+        assert rc == 0, emb.last_error()
+        torch.cuda.synchronize()
+        assert_close(out.cpu().numpy(), ref, name)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_head_dims_and_ragged_batch(emb, orc, torch_dev, d):
+    """Ragged batch: query counts 1..70 (partial row tiles), key counts not multiples of 16."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(d)
+    nq = [1, 17, 70, 33]
+    nk = [5, 77, 300, 129]
+    s = Seqs(orc, rng, nk, nq, 4, 2, d)
+    got = s.run(emb, torch, dev, 1 / math.sqrt(d))
+    for b in range(len(nq)):
+        assert_close(got[b], s.oracle(orc, b, 1 / math.sqrt(d)), f"d={d} b={b}")
+    got3 = s.run(emb, torch, dev, 1 / math.sqrt(d), splits=3)
+    for b in range(len(nq)):
+        assert_close(got3[b], s.oracle(orc, b, 1 / math.sqrt(d)), f"d={d} b={b} split 3")

@@ -1,0 +1,169 @@
+"""CPU tests of libemb_kv.so: exports, host-side cache/page/flex logic vs the
+oracle, and argument checks that return before any GPU work."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+
+def test_library_exports_every_header_symbol(emb):
+    syms = emb.header_symbols()
+    assert len(syms) > 40
+    missing = [s for s in syms if not hasattr(emb.lib(), s)]
+    assert not missing, missing
+    assert b"gfx950" in emb.lib().emb_version()
+
+
+def _ops(rng, n_ops, cap):
+    ops = []
+    for _ in range(n_ops):
+        r = rng.random()
+        k = int(rng.integers(1, max(2, cap // 3)))
+        if r < 0.45:
+            ops.append(("update", k, int(rng.random() < 0.3)))
+        elif r < 0.7:
+            ops.append(("mode0", k, 0))
+        elif r < 0.8:
+            ops.append(("clear_pred", 0, 0))
+        elif r < 0.9:
+            ops.append(("update_restore", k, 0))
+        else:
+            ops.append(("chunk", cap // 4, 0))
+    return ops
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("legacy", [False, True])
+def test_slot_cache_matches_oracle(emb, orc, seed, legacy):
+    rng = np.random.default_rng(seed)
+    cap = int(rng.integers(8, 60))
+    a = emb.SlotCache(cap, legacy)
+    b = orc.Cache(cap, legacy)
+    for op, k, pred in _ops(rng, 60, cap):
+        if op in ("update", "chunk"):
+            sa, rc = a.update_meta(k, pred)
+            sb = b.update_meta(k, pred)
+            assert (rc == 0) == (sb is not None)
+            if sb is not None:
+                assert np.array_equal(sa, sb)
+        elif op == "update_restore":
+            sa, rc = a.update_meta(k, 0)
+            sb = b.update_meta(k, 0)
+            assert (rc == 0) == (sb is not None)
+            if sb is not None:
+                a.restore(sa)
+                b.restore(sb)
+        elif op == "mode0":
+            sa, va, rc = a.prepare_mode0(k)
+            sb, vb = b.prepare_mode0(k)
+            assert (rc == 0) == (sb is not None)
+            if sb is not None:
+                assert np.array_equal(sa, sb) and np.array_equal(va, vb)
+        else:
+            a.clear_pred()
+            b.clear_pred()
+        ia, ma, pa = a.state()
+        ib, mb, pb = b.state()
+        assert np.array_equal(ia, ib) and np.array_equal(ma, mb) and np.array_equal(pa, pb), op
+        assert a.used_count() == b.used_count() and a.pred_count() == b.pred_count()
+        assert a.next_id() == b.next_id()
+        assert np.array_equal(a.collect_valid(), b.collect_valid())
+
+
+def test_page_pool_and_block_table(emb):
+    pool = emb.PagePool(20, seed=7)
+    c = emb.SlotCache(64)
+    c.bind_pool(pool)
+    assert pool.free_count() == 20
+    s, rc = c.update_meta(20, 0)          # slots 0..19 -> pages for logical pages 0, 1
+    assert rc == 0 and list(s) == list(range(20))
+    bt = c.block_table()
+    assert bt.shape == (4,) and bt[0] >= 0 and bt[1] >= 0 and bt[2] == -1 and bt[3] == -1
+    assert pool.free_count() == 18 and bt[0] != bt[1]
+    c.map_range(64)
+    bt = c.block_table()
+    assert np.all(bt >= 0) and len(set(bt.tolist())) == 4 and pool.free_count() == 16
+    c2 = emb.SlotCache(300)
+    c2.bind_pool(pool)
+    _, rc = c2.update_meta(300, 0)          # needs 19 pages, 16 left
+    assert rc == -3 and "exhausted" in emb.last_error()
+    assert c2.used_count() == 0 and pool.free_count() == 0  # mapped pages stay with c2
+    c.release_pages()
+    assert pool.free_count() == 4
+    c2.release_pages()
+    assert pool.free_count() == 20
+    # a seeded pool hands out a permutation; seed 0 hands out 0, 1, 2, ...
+    p0 = emb.PagePool(8, seed=0)
+    c3 = emb.SlotCache(128)
+    c3.bind_pool(p0)
+    c3.map_range(128)
+    assert list(c3.block_table()) == list(range(8))
+
+
+def test_capacity_matches_oracle(emb, orc):
+    for kw in [dict(seq=100), dict(frame_chunk_size=2, action_per_frame=16, attn_window=72,
+                                   latent_h=24, latent_w=20, seq=10),
+               dict(override_tokens=14040, seq=1560), dict(patch_t=0, seq=1), dict(seq=99999),
+               dict(n_suffix=7, attn_window=9, seq=3)]:
+        assert emb.lingbot_kv_capacity(**kw) == orc.lingbot_capacity(**kw), kw
+
+
+def test_flex_meta_tables_match_oracle(emb, orc):
+    L = emb.lib()
+    for args in [(1, 2, 2, 2, 1, 2, 1, 1, 1, 1, 4, 1, 1, 1, 5, 4),
+                 (1, 4, 4, 4, 1, 4, 2, 1, 3, 2, 1, 2, 2, 2, 7, 8),
+                 (2, 2, 2, 4, 1, 2, 2, 1, 0, 1, 0, 1, 1, 2, 3, 4)]:
+        m = L.emb_flex_meta_build(*args)
+        om = orc.FlexMeta(*args)
+        n = L.emb_flex_meta_len(m)
+        for q in range(n):
+            for k in range(n):
+                assert L.emb_flex_self_allowed(m, q, k) == orc.lib().orc_flex_self_allowed(om.h, q, k)
+        bs = args[-1]
+        qb = (n + bs - 1) // bs
+        rp = np.zeros(qb + 1, np.int32)
+        ci = np.zeros(qb * qb, np.int32)
+        nnz = L.emb_self_block_table(m, rp.ctypes.data_as(emb.i32p), ci.ctypes.data_as(emb.i32p))
+        orp, oci = orc.self_block_table(om, n, bs)
+        assert np.array_equal(rp, orp) and np.array_equal(ci[:nnz], oci)
+        tm = np.zeros(n * n, np.uint8)
+        L.emb_self_token_mask(m, tm.ctypes.data_as(emb.u8p))
+        assert np.array_equal(tm.reshape(n, n), orc.self_token_mask(om, n))
+        L.emb_flex_meta_destroy(m)
+    rp = np.zeros(4, np.int32)
+    ci = np.zeros(12, np.int32)
+    assert L.emb_dense_block_table(9, 13, 4, rp.ctypes.data_as(emb.i32p), ci.ctypes.data_as(emb.i32p)) == 12
+
+
+def test_synthetic_generator_matches_oracle(emb, orc):
+    for seed, n in [(0xE3BD0001, 1001), (0xE3BD0003, 4096)]:
+        assert np.array_equal(emb.synth_normal_bf16(seed, n), orc.normal_bf16(seed, n))
+
+
+def test_device_entry_points_reject_bad_arguments(emb):
+    L = emb.lib()
+    # every check below returns before any HIP call, so it runs without a GPU
+    assert L.emb_kv_append(None, None, 0, 1, None, None, 16, None, None, 1, 128, None) == -1
+    assert "null" in emb.last_error()
+    buf = C.c_void_p(256)  # aligned, never dereferenced: rejected on shape first
+    assert L.emb_kv_append(buf, buf, 100, 4, buf, None, 16, buf, buf, 1, 100, None) == -1
+    assert "multiple of 8" in emb.last_error()
+    assert L.emb_kv_gather(buf, buf, buf, 0, None, 16, buf, buf, 1, 128, None) == -1
+    assert L.lingbot_runtime_kv_update_f32(buf, buf, buf, buf, buf, 4, 1, 64, 4, None) == -1
+    assert "capacity" in emb.last_error()
+    with pytest.raises(RuntimeError, match="head_dim"):
+        emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=1, hq=8, hkv=1, d=96,
+                            max_q=4, scale=0.1, capacity=64)
+    with pytest.raises(RuntimeError, match="head counts"):
+        emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=1, hq=6, hkv=4, d=128,
+                            max_q=4, scale=0.1, capacity=64)
+    with pytest.raises(RuntimeError, match="cu_q"):
+        emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=2, hq=8, hkv=1, d=128,
+                            max_q=4, scale=0.1, capacity=64)
+    with pytest.raises(RuntimeError, match="workspace"):
+        emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=1, hq=8, hkv=1, d=128,
+                            max_q=4, scale=0.1, capacity=64, splits=4)
+    assert L.lingbot_runtime_kv_attn_f32(None, None, None, None, None, 1, 1, 1, 64, 0.1, None) == -1
+    assert emb.attn_workspace_bytes(1, 51, 8, 1, 256, 4) == 4 * 512 * (256 + 2) * 4

@@ -1,0 +1,349 @@
+"""Pins the CPU oracle (oracle/emb_oracle.c) before it is trusted as the checker.
+
+Each test is a known answer derived by hand from the reference's documented
+semantics, a known answer the reference itself holds, an invariant, or a
+reduction to a library routine (numpy) -- chosen so that a plausible slip
+(wrong index, swapped operand, dropped term) fails.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+
+# ---------------- random generation ----------------
+def test_mt19937_64_known_answer(orc):
+    # C++ standard [rand.predef]: the 10000th output of a default-constructed
+    # std::mt19937_64 (seed 5489) is 9981545732273789042.
+    assert orc.lib().orc_mt64_nth(5489, 10000) == 9981545732273789042
+
+
+def test_bf16_round_to_nearest_even(orc):
+    import torch
+    L = orc.lib()
+    assert L.orc_f32_to_bf16(1.0) == 0x3F80
+    assert L.orc_f32_to_bf16(1.0 + 2.0 ** -8) == 0x3F80          # tie -> even
+    assert L.orc_f32_to_bf16(1.0 + 3 * 2.0 ** -8) == 0x3F82      # tie -> even (up)
+    assert L.orc_f32_to_bf16(-2.5) == 0xC020
+    x = np.random.default_rng(1).standard_normal(20000).astype(np.float32) * 37
+    ours = orc.f32_to_bf16(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, ref)
+    assert np.array_equal(np.array([L.orc_f32_to_bf16(float(v)) for v in x[:500]], np.uint16), ref[:500])
+
+
+def test_normal_generator_statistics(orc):
+    z = orc.bf16_to_f32(orc.normal_bf16(0xE3BD0001, 400000)).astype(np.float64)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
+    assert abs(np.mean(np.abs(z) < 1.0) - 0.6827) < 0.005  # one-sigma mass
+
+
+# ---------------- slot cache: hand-derived scenarios ----------------
+def test_slot_cache_fill_and_whole_chunk_eviction(orc):
+    c = orc.Cache(6)
+    assert list(c.update_meta(2, 0)) == [0, 1] and c.next_id() == 1
+    assert list(c.update_meta(2, 1)) == [2, 3]
+    assert list(c.update_meta(2, 0)) == [4, 5]
+    ids, m, pr = c.state()
+    assert list(ids) == [0, 0, 1, 1, 2, 2] and list(m) == [1] * 6 and list(pr) == [0, 0, 1, 1, 0, 0]
+    # full: the oldest chunk (id 0, slots 0-1) is evicted; the new id is max+1
+    assert list(c.update_meta(2, 0)) == [0, 1]
+    ids, m, pr = c.state()
+    assert list(ids) == [3, 3, 1, 1, 2, 2]
+    # valid slots are in ascending slot order, not age order
+    assert list(c.collect_valid()) == [0, 1, 2, 3, 4, 5]
+    assert c.used_count() == 6 and c.pred_count() == 2
+
+
+def test_slot_cache_clear_pred_and_mode0(orc):
+    c = orc.Cache(8)
+    c.update_meta(3, 0)      # slots 0-2 id 0
+    c.update_meta(2, 1)      # slots 3-4 id 1 (pred)
+    c.clear_pred()           # non-legacy: mask 0, id/is_pred kept
+    ids, m, pr = c.state()
+    assert list(m) == [1, 1, 1, 0, 0, 0, 0, 0]
+    assert list(ids[:5]) == [0, 0, 0, 1, 1] and list(pr[:5]) == [0, 0, 0, 1, 1]
+    assert c.pred_count() == 0 and c.next_id() == 1
+    s, v = c.prepare_mode0(2)  # temp slots 3-4, id 1, invisible afterwards
+    assert list(s) == [3, 4] and list(v) == [0, 1, 2, 3, 4]
+    ids, m, pr = c.state()
+    assert list(m) == [1, 1, 1, 0, 0, 0, 0, 0] and list(ids[3:5]) == [1, 1] and list(pr[3:5]) == [0, 0]
+    assert list(c.collect_valid()) == [0, 1, 2]
+
+
+def test_slot_cache_legacy_clear_pred(orc):
+    c = orc.Cache(4, legacy=True)
+    c.update_meta(2, 1)
+    c.clear_pred()
+    ids, m, pr = c.state()
+    assert list(ids) == [-1] * 4 and list(m) == [0] * 4 and list(pr) == [0] * 4
+
+
+def test_slot_cache_eviction_tie_rule_and_failure(orc):
+    c = orc.Cache(4)
+    c.update_meta(3, 0)  # slots 0-2 id 0
+    # need 2 more with 1 free: evict ONE of the id-0 slots.  std::sort leaves the
+    # choice open in the reference; the oracle takes the lowest slot.
+    assert list(c.update_meta(2, 0)) == [0, 3]
+    ids, m, _ = c.state()
+    assert list(ids) == [1, 0, 0, 1]
+    # a request larger than capacity fails, after evicting everything
+    assert c.update_meta(5, 0) is None
+    assert c.used_count() == 0
+
+
+def test_slot_cache_mode0_restore_keeps_ids(orc):
+    c = orc.Cache(4)
+    c.update_meta(2, 0)
+    s = c.update_meta(2, 0)   # mode-0 without the fast path: insert then restore
+    c.restore(s)
+    ids, m, _ = c.state()
+    assert list(m) == [1, 1, 0, 0] and list(ids) == [0, 0, 1, 1]
+    assert c.next_id() == 1
+
+
+def test_lingbot_capacity_known_answers(orc):
+    # LIBERO defaults (models/lingbot_va.cpp:9231-9248): window 30, 4 frames a
+    # chunk, 4 actions a frame, latent 8x16, patch (1,2,2):
+    # latent tokens 4*8*16/4 = 128, action tokens 16 -> 15*128 + 15*16 = 2160.
+    assert orc.lingbot_capacity(seq=100) == 2160
+    # robotwin_tshape: window 72, 2 frames, 16 actions, latent 24x20:
+    # latent 2*24*20/4 = 240, action 32 -> 36*240 + 36*32 = 9792
+    assert orc.lingbot_capacity(frame_chunk_size=2, action_per_frame=16, attn_window=72,
+                                latent_h=24, latent_w=20, seq=10) == 9792
+    assert orc.lingbot_capacity(seq=5000) == 5000                    # never below seq
+    assert orc.lingbot_capacity(override_tokens=14040, seq=1560) == 14040
+    assert orc.lingbot_capacity(override_tokens=100, seq=1560) == 1560
+    assert orc.lingbot_capacity(patch_t=0, seq=1) == 15 * 128 + 15 * 16  # 128-token default
+
+
+# ---------------- paged layout == token-slot layout (bit-exact chain) ----------------
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_paged_matches_slot_semantics(orc, seed):
+    rng = np.random.default_rng(seed)
+    H, D, cap = 3, 16, 70
+    n = 40
+    k = rng.integers(0, 65535, (n, H, D), dtype=np.uint16)
+    v = rng.integers(0, 65535, (n, H, D), dtype=np.uint16)
+    slots = rng.choice(np.arange(-3, cap + 3), n, replace=False).astype(np.int32)
+    n_pages = (cap + 15) // 16
+    bt = rng.permutation(n_pages + 5)[:n_pages].astype(np.int32)
+    ck = np.zeros((cap, H, D), np.uint16)
+    cv = np.zeros((cap, H, D), np.uint16)
+    orc.slot_update(k, v, ck, cv, slots, H, D, cap)
+    kp = np.zeros(((n_pages + 5) * H * 16 * D,), np.uint16)
+    vpool = np.zeros_like(kp)
+    orc.paged_append(k, v, H * D, slots, bt, H, D, cap, kp, vpool)
+    valid = np.sort(slots[(slots >= 0) & (slots < cap)])
+    valid = np.concatenate([valid, [-1, cap]]).astype(np.int32)  # out-of-range rows untouched
+    g1k = np.full((len(valid), H, D), 7, np.uint16); g1v = g1k.copy()
+    g2k = g1k.copy(); g2v = g1k.copy()
+    orc.slot_gather(ck, cv, valid, H, D, cap, g1k, g1v)
+    orc.paged_gather(kp, vpool, valid, bt, H, D, cap, g2k, g2v)
+    assert np.array_equal(g1k, g2k) and np.array_equal(g1v, g2v)
+    # the gathered rows are exactly the appended source rows
+    src_of = {int(s): i for i, s in enumerate(slots)}
+    for i, s in enumerate(valid[:-2]):
+        assert np.array_equal(g2k[i], k[src_of[int(s)]]) and np.array_equal(g2v[i], v[src_of[int(s)]])
+    assert np.all(g2k[-2:] == 7)
+    # layout: K row t of page p is contiguous; V is stored [d][t]
+    s0 = int(valid[0]); p0 = int(bt[s0 // 16]); t0 = s0 % 16
+    base = (p0 * H + 1) * 16 * D
+    assert np.array_equal(kp[base + t0 * D: base + (t0 + 1) * D], k[src_of[s0], 1])
+    assert vpool[(p0 * H + 1) * D * 16 + 5 * 16 + t0] == v[src_of[s0], 1, 5]
+
+
+# ---------------- flex masks ----------------
+def _small_meta(orc, window=4):
+    # latent (b=1, f=2, h=2, w=2), patch 1 -> 8 tokens a copy, frames (f*1)/1*2 = {0, 2};
+    # action (f=2, h=1, w=1) -> frames f*2+1 = {1, 3}; padding 1.
+    # order: latent noisy [0,8), latent clean [8,16), action noisy 16-17,
+    # action clean 18-19, pad 20.
+    return orc.FlexMeta(1, 2, 2, 2, 1, 2, 1, 1, 1, 1, window, 1, 1, 1, 5, 4)
+
+
+def test_flex_predicate_known_answers(orc):
+    m = _small_meta(orc)
+    A = lambda q, k: orc.lib().orc_flex_self_allowed(m.h, q, k)
+    assert A(4, 8) == 1      # noisy f2 -> clean f0: noise2clean needs kf < qf
+    assert A(4, 12) == 0     # noisy f2 -> clean f2: not strictly earlier
+    assert A(4, 5) == 1      # noisy f2 -> noisy f2: same frame
+    assert A(4, 0) == 0      # noisy f2 -> noisy f0
+    assert A(12, 8) == 1     # clean f2 -> clean f0: clean2clean kf <= qf
+    assert A(12, 13) == 1    # clean -> clean same frame
+    assert A(8, 12) == 0     # clean f0 -> clean f2: future
+    assert A(8, 0) == 0      # clean never sees noisy
+    assert A(16, 8) == 1     # action noisy f1 -> latent clean f0
+    assert A(16, 12) == 0    # action noisy f1 -> latent clean f2 (future)
+    assert A(18, 19) == 0    # action clean f1 -> action clean f3
+    assert A(19, 18) == 1
+    assert A(20, 20) == 0 and A(3, 20) == 0   # padding sees and is seen by nothing
+    m1 = _small_meta(orc, window=1)
+    assert orc.lib().orc_flex_self_allowed(m1.h, 12, 8) == 0  # |2-0| > window
+    assert orc.lib().orc_flex_cross_allowed(m.h, 3, 4) == 1
+    assert orc.lib().orc_flex_cross_allowed(m.h, 20, 0) == 0
+
+
+def test_flex_block_tables_brute_force(orc):
+    m = _small_meta(orc)
+    n, bs = 21, 4
+    tm = orc.self_token_mask(m, n)
+    rp, ci = orc.self_block_table(m, n, bs)
+    qb = (n + bs - 1) // bs
+    for r in range(qb):
+        want = [c for c in range(qb) if tm[r * bs:(r + 1) * bs, c * bs:(c + 1) * bs].any()]
+        assert list(ci[rp[r]:rp[r + 1]]) == want
+    rp, ci = orc.dense_block_table(9, 13, 4)
+    assert list(rp) == [0, 4, 8, 12] and list(ci) == [0, 1, 2, 3] * 3
+    rp, ci = orc.cross_block_table(m, n, 5, bs)
+    assert list(ci[rp[5]:rp[6]]) == []         # block 5 holds only the pad token
+    assert orc.lib().orc_max_row_nnz(rp.ctypes.data_as(orc.i64p), qb) == 2
+
+
+# ---------------- attention ----------------
+def _smoke_inputs():
+    # lingbot_flex_attn_cuda_smoke, kernels/lingbot/lingbot_flex_attn_cuda.cu:1033-1048
+    S, H, D = 8, 2, 8
+    i = np.arange(S * H * D, dtype=np.float32)
+    q = (np.sin(i * np.float32(0.017)) * np.float32(0.2)).astype(np.float32)
+    k = (np.cos(i * np.float32(0.019)) * np.float32(0.15)).astype(np.float32)
+    v = (np.sin(i * np.float32(0.023)) * np.float32(0.3)).astype(np.float32)
+    s, t = np.meshgrid(np.arange(S), np.arange(S), indexing="ij")
+    mask = ((t <= s) & (s - t <= 4)).astype(np.uint8)
+    return S, H, D, q, k, v, mask
+
+
+def test_reference_flex_smoke_known_answer(orc):
+    S, H, D, q, k, v, mask = _smoke_inputs()
+    scale = 1.0 / math.sqrt(D)
+    dense = orc.dense_masked_attention(q, k, v, mask, S, H, D)
+    flex = orc.flex_attention(q, k, v, [0, 1, 3], [0, 0, 1], mask, S, S, H, D, 4, scale)
+    assert np.abs(flex - dense).max() < 1e-5  # the reference's own pass criterion
+    # and the same numbers from numpy's softmax over a masked score matrix
+    qh, kh, vh = (x.reshape(S, H, D).astype(np.float64) for x in (q, k, v))
+    sc = np.einsum("shd,thd->hst", qh, kh) * scale
+    sc = np.where(mask[None].astype(bool), sc, -np.inf)
+    p = np.exp(sc - sc.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    ref = np.einsum("hst,thd->shd", p, vh).reshape(-1)
+    assert np.abs(dense - ref).max() < 1e-6
+
+
+def _np_attention(q, k, v, hq, hkv, scale, allow=None, add=None):
+    """softmax(q k^T * scale + add) v with numpy matmul; q [nq,hq,d], k/v [nk,hkv,d]."""
+    G = hq // hkv
+    qh = q.astype(np.float64).transpose(1, 0, 2)
+    kh = np.repeat(k.astype(np.float64).transpose(1, 0, 2), G, axis=0)
+    vh = np.repeat(v.astype(np.float64).transpose(1, 0, 2), G, axis=0)
+    s = qh @ kh.transpose(0, 2, 1) * scale
+    if add is not None:
+        s = s + add[None]
+    if allow is not None:
+        s = np.where(allow[None].astype(bool), s, -np.inf)
+    mx = s.max(-1, keepdims=True)
+    mx = np.where(np.isfinite(mx), mx, 0)
+    p = np.exp(s - mx)
+    den = p.sum(-1, keepdims=True)
+    o = (p @ vh) / np.where(den > 0, den, 1)
+    o = np.where(den > 0, o, 0)
+    return o.transpose(1, 0, 2)
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 1), (8, 2), (4, 4)])
+def test_gqa_oracle_matches_numpy(orc, hq, hkv):
+    rng = np.random.default_rng(hq * 10 + hkv)
+    nq, nk, d = 5, 23, 32
+    qb = orc.f32_to_bf16(rng.standard_normal((nq, hq, d)).astype(np.float32))
+    kb = orc.f32_to_bf16(rng.standard_normal((nk, hkv, d)).astype(np.float32))
+    vb = orc.f32_to_bf16(rng.standard_normal((nk, hkv, d)).astype(np.float32))
+    allow = (rng.random((nq, nk)) < 0.7).astype(np.uint8)
+    allow[2] = 0  # an empty row gives 0
+    add = rng.standard_normal((nq, nk)).astype(np.float32)
+    scale = 1 / math.sqrt(d)
+    out = orc.gqa_attention(qb, kb, vb, nq, nk, hq, hkv, d, scale, allow=allow, add=add)
+    ref = _np_attention(orc.bf16_to_f32(qb), orc.bf16_to_f32(kb), orc.bf16_to_f32(vb), hq, hkv,
+                        scale, allow=allow, add=add)
+    assert np.abs(out - ref).max() < 1e-5
+    assert np.all(out[2] == 0)
+
+
+def test_gqa_head_mapping_and_special_cases(orc):
+    # q = 0 gives uniform weights: each q head returns the mean V of its kv head,
+    # and q head h must read kv head h // (hq/hkv).
+    nq, nk, hq, hkv, d = 3, 6, 8, 2, 16
+    q = np.zeros((nq, hq, d), np.uint16)
+    v = np.zeros((nk, hkv, d), np.float32)
+    v[:, 0] = np.arange(nk)[:, None]          # mean 2.5
+    v[:, 1] = -np.arange(nk)[:, None] * 2     # mean -5
+    k = orc.f32_to_bf16(np.random.default_rng(0).standard_normal((nk, hkv, d)).astype(np.float32))
+    out = orc.gqa_attention(q, k, orc.f32_to_bf16(v), nq, nk, hq, hkv, d, 0.1)
+    assert np.allclose(out[:, :4], 2.5) and np.allclose(out[:, 4:], -5.0)
+    # a single visible key returns that key's V row exactly
+    allow = np.zeros((nq, nk), np.uint8)
+    allow[:, 3] = 1
+    out = orc.gqa_attention(q, k, orc.f32_to_bf16(v), nq, nk, hq, hkv, d, 0.1, allow=allow)
+    assert np.all(out[:, :4] == 3.0) and np.all(out[:, 4:] == -6.0)
+    # chunk-causal rule on positions: chunk 2, queries at positions 4..6 of 6 keys
+    # (q_pos0 = nk - nq = 3): position p sees keys j with j//2 <= p//2.
+    out_c = orc.gqa_attention(q, k, orc.f32_to_bf16(v), nq, nk, hq, hkv, d, 0.1, chunk=2)
+    vis = [[j for j in range(nk) if j // 2 <= (3 + i) // 2] for i in range(nq)]
+    for i in range(nq):
+        assert np.allclose(out_c[i, 0], np.mean(vis[i])), (i, out_c[i, 0, 0])
+
+
+def test_runtime_kv_attention_quirk(orc):
+    # online/warp kernels: a negative slot adds exp(0 - max) to the denominator
+    # and no V row.  With q = 0 every score is 0: out = sum(v_valid) / n_all.
+    H, D, cap = 2, 8, 5
+    q = np.zeros(1 * H * D, np.float32)
+    ck = np.random.default_rng(3).standard_normal(cap * H * D).astype(np.float32)
+    cv = np.arange(cap * H * D, dtype=np.float32) % 7
+    valid = [4, -1, 1]
+    out = orc.runtime_kv_attn(q, ck, cv, valid, 1, H, D, 0.3).reshape(H, D)
+    cvr = cv.reshape(cap, H, D)
+    assert np.allclose(out, (cvr[4] + cvr[1]) / 3)
+    out2 = orc.runtime_kv_attn(q, ck, cv, valid, 1, H, D, 0.3, online_quirk=False).reshape(H, D)
+    assert np.allclose(out2, (cvr[4] + cvr[1]) / 2)
+
+
+# ---------------- W8 Marlin layout and numerics ----------------
+def test_marlin_dst_byte_known_answers(orc):
+    f = lambda k, n, N=128: orc.lib().orc_marlin_dst_byte(k, n, N)
+    # kernels/cosmos3/README.md:55-64 evaluated by hand
+    assert f(0, 0) == 0
+    assert f(1, 0) == 2          # lane (k%2)*2
+    assert f(8, 0) == 1          # lane (k/8)%2
+    assert f(9, 0) == 3
+    assert f(2, 0) == 32         # col ((k%8)/2)*8 = 8 -> byte 32
+    assert f(0, 1) == 128        # col (n%8)*32 = 32
+    assert f(0, 8) == 4          # col (n/8)%8 = 1
+    assert f(0, 64) == 1024      # col (n/64)*256
+    assert f(16, 0) == 16 * 128  # next 16-row band: row*(N*4) words
+    K, N = 32, 128
+    bytes_ = sorted(f(k, n, N) for k in range(K) for n in range(N))
+    assert bytes_ == list(range(K * N))  # a bijection onto the packed payload
+
+
+def test_marlin_scale_permutation(orc):
+    si = orc.lib().orc_marlin_scale_index
+    assert [si(n) for n in (0, 1, 2, 8, 9, 31, 32, 34)] == [0, 1, 8, 2, 3, 31, 32, 40]
+    assert sorted(si(n) for n in range(96)) == list(range(96))
+
+
+def test_marlin_pack_unpack_and_gemm(orc):
+    rng = np.random.default_rng(5)
+    K, N, M = 64, 128, 7
+    w = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    q = orc.marlin_pack_w8(w)
+    assert q.shape == (K // 16, 4 * N)
+    for k, n in [(0, 0), (5, 77), (63, 127), (17, 64)]:
+        assert orc.marlin_unpack_w8(q, K, N, k, n) == w[k, n]
+    s = orc.f32_to_bf16(rng.uniform(0.001, 0.01, N).astype(np.float32))
+    s_st = orc.marlin_pack_scales(s)
+    x = orc.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    yb, yf = orc.w8a16_gemm(x, q, s_st, M, K, N)
+    ref = (orc.bf16_to_f32(x).astype(np.float64) @ w.astype(np.float64)) * orc.bf16_to_f32(s)[None].astype(np.float64)
+    assert np.allclose(yf, ref, rtol=1e-6, atol=1e-5)
+    assert np.array_equal(yb, orc.f32_to_bf16(yf))
