@@ -21,6 +21,7 @@
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct MoveGeom {
     int32_t n;          // tokens
@@ -50,14 +51,16 @@ __device__ __forceinline__ void load8<uint16_t>(const uint16_t *p, uint16_t (&o)
     }
 }
 
+// Loaded as float vectors: hipcc 7.2 folds __builtin_bit_cast(float, v[i]) of
+// an ext-vector element to element 0 for every i, so no element is bit-cast.
 template <>
 __device__ __forceinline__ void load8<float>(const float *p, uint16_t (&o)[8]) {
-    const u32x4 a = *reinterpret_cast<const u32x4 *>(p);
-    const u32x4 b = *reinterpret_cast<const u32x4 *>(p + 4);
+    const f32x4 a = *reinterpret_cast<const f32x4 *>(p);
+    const f32x4 b = *reinterpret_cast<const f32x4 *>(p + 4);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        o[i] = bf16_rne(__builtin_bit_cast(float, a[i]));
-        o[4 + i] = bf16_rne(__builtin_bit_cast(float, b[i]));
+        o[i] = bf16_rne(a[i]);
+        o[4 + i] = bf16_rne(b[i]);
     }
 }
 

@@ -113,6 +113,14 @@ def lib():
     if _lib is None:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        # torch ships its own libamdhip64.so.7.  Loading torch first makes this
+        # library bind to that same runtime (the dynamic linker matches the
+        # soname), so device pointers and streams from torch are valid here; a
+        # second HIP runtime in the process would not see the device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(str(LIB_PATH))
         for name, (res, args) in _SIGS.items():
             f = getattr(L, name)
