@@ -1,0 +1,512 @@
+"""Benchmark of the KV-cached attention step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs cfg1,cfg2,cfg3,cfg4]
+                    [--no-cpu] [--only cfg1_attn]
+
+Headline (the JSON line's `value`): BASELINE.json configs[0] -- the pi0.5
+action-expert denoise step: 18 layers, each with an 816-token cached prefix
+(1 kv head, head_dim 256, bf16) in 16-token pages scattered over one pool,
+fresh Q [51 tokens x 8 heads] and fresh action K/V [51] per layer per step.
+One step = one append launch (51 new K/V rows into every layer's temporary
+slots 816..866) + one attention launch over the 18 layers' (51x8) x 867
+problems, replayed from a HIP graph.  Unit: microseconds per denoise step.
+
+Other configs run as extra measurements in the same JSON object ("extra").
+All inputs are synthetic N(0,1) bf16 from the library's std::mt19937_64
+generator (seed 0xE3BD0000 + config index), uploaded before timing starts.
+The CPU baseline times the oracle's fp32 restatement of the ggml op order on
+host cores (bounded sample, see `cpu_baseline.sample`).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "embodied.cpp_amd"))
+
+PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+class Ctx:
+    def __init__(self):
+        import torch
+
+        import embkv
+
+        self.torch = torch
+        self.emb = embkv
+        embkv.lib()
+        self.dev = torch.device("cuda:0")
+        self.stream = torch.cuda.current_stream()
+
+    def synth(self, seed, n):
+        """N(0,1) bf16 from the library generator, as an int16 device tensor."""
+        return self.torch.from_numpy(self.emb.synth_normal_bf16(seed, n).view(np.int16)).to(self.dev)
+
+    def i32(self, a):
+        return self.torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(self.dev)
+
+    def time_graph(self, fn, steps, warmup):
+        """Captures fn() once into a HIP graph; replays warmup + steps times.
+        Returns (ms per replay, graph) measured with events on the replay stream."""
+        torch = self.torch
+        fn(torch.cuda.current_stream())  # eager once (also validates arguments)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                fn(s)
+        torch.cuda.synchronize()
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        cur = torch.cuda.current_stream()
+        e0.record(cur)
+        for _ in range(steps):
+            g.replay()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps, g
+
+
+# ---------------------------------------------------------------------------
+# cfg1: pi0.5 action expert over the cached prefix (denoise steps)
+# ---------------------------------------------------------------------------
+class PagedLayers:
+    """L independent caches (layers or sessions) sharing one permuted page pool.
+    Cache b holds n_keys[b] slots: a prefix plus n_new temporary slots."""
+
+    def __init__(self, c: Ctx, seed, n_prefix, n_new, hq, hkv, d, n_steps, extra_pages=64):
+        torch, emb = c.torch, c.emb
+        self.c = c
+        self.L = len(n_prefix)
+        self.n_prefix = [int(x) for x in n_prefix]
+        self.n_new, self.hq, self.hkv, self.d = n_new, hq, hkv, d
+        self.n_keys = [p + n_new for p in self.n_prefix]
+        pages = [(k + 15) // 16 for k in self.n_keys]
+        self.bt_stride = max(pages)
+        self.cap = self.bt_stride * 16
+        total_pages = sum(pages) + extra_pages
+        g = np.random.default_rng(seed)
+        perm = g.permutation(total_pages).astype(np.int32)
+        bt = np.full((self.L, self.bt_stride), -1, np.int32)
+        o = 0
+        for b, p in enumerate(pages):
+            bt[b, :p] = perm[o:o + p]
+            o += p
+        self.bt_np = bt
+        self.bt = c.i32(bt)
+        self.total_pages = total_pages
+        page_elems = hkv * 16 * d
+        self.k_pool = torch.zeros(total_pages * page_elems, dtype=torch.int16, device=c.dev)
+        self.v_pool = torch.zeros_like(self.k_pool)
+        # prefix K/V appended through the library (one combined slot space:
+        # cache b's slot s is logical slot b*cap + s of one concatenated table)
+        tot_pref = sum(self.n_prefix)
+        if tot_pref:
+            kpre = c.synth(seed + 1, tot_pref * hkv * d)
+            vpre = c.synth(seed + 2, tot_pref * hkv * d)
+            slots = np.concatenate([b * self.cap + np.arange(p) for b, p in enumerate(self.n_prefix)])
+            emb.kv_append(kpre, vpre, hkv * d, tot_pref, c.i32(slots), self.bt, self.L * self.cap,
+                          self.k_pool, self.v_pool, hkv, d)
+        # per-step new K/V and Q
+        self.new_slots = c.i32(np.concatenate([b * self.cap + p + np.arange(n_new)
+                                               for b, p in enumerate(self.n_prefix)]))
+        self.n_steps = n_steps
+        self.q = [c.synth(seed + 10 + s, self.L * n_new * hq * d) for s in range(n_steps)]
+        self.knew = [c.synth(seed + 100 + s, self.L * n_new * hkv * d) for s in range(n_steps)]
+        self.vnew = [c.synth(seed + 200 + s, self.L * n_new * hkv * d) for s in range(n_steps)]
+        self.cu_q = c.i32(np.arange(self.L + 1) * n_new)
+        self.nk = c.i32(self.n_keys)
+        self.out = torch.zeros((self.L * n_new, hq, d), dtype=torch.float32, device=c.dev)
+        self.ws = None
+        torch.cuda.synchronize()
+
+    def set_splits(self, splits):
+        self.splits = splits
+        if splits > 1:
+            nb = self.c.emb.attn_workspace_bytes(self.L, self.n_new, self.hq, self.hkv, self.d, splits)
+            self.ws = self.c.torch.empty(nb // 4 + 64, dtype=self.c.torch.float32, device=self.c.dev)
+
+    def append(self, step, stream):
+        s = step % self.n_steps
+        self.c.emb.kv_append(self.knew[s], self.vnew[s], self.hkv * self.d, self.L * self.n_new,
+                             self.new_slots, self.bt, self.L * self.cap, self.k_pool, self.v_pool,
+                             self.hkv, self.d, stream=stream)
+
+    def attend(self, step, stream, scale):
+        s = step % self.n_steps
+        self.c.emb.paged_attention(q=self.q[s], out=self.out, k_pool=self.k_pool, v_pool=self.v_pool,
+                                   batch=self.L, hq=self.hq, hkv=self.hkv, d=self.d, max_q=self.n_new,
+                                   scale=scale, capacity=self.cap, cu_q=self.cu_q, n_keys=self.nk,
+                                   block_tables=self.bt, bt_stride=self.bt_stride, splits=self.splits,
+                                   workspace=self.ws, stream=stream)
+
+    # algorithmic bytes of one attention launch: K/V of every key once, Q, O (f32), tables
+    def attn_bytes(self):
+        kv = sum(self.n_keys) * self.hkv * self.d * 2 * 2
+        q = self.L * self.n_new * self.hq * self.d * 2
+        o = self.L * self.n_new * self.hq * self.d * 4
+        return kv + q + o + self.L * self.bt_stride * 4
+
+    def attn_flops(self):
+        return sum(4.0 * self.n_new * self.hq * k * self.d for k in self.n_keys)
+
+    def survey_step_bytes(self):
+        """Per-unit algorithmic bytes as defined for configs 1/4: prefix K/V,
+        new K/V read + written, Q and O at bf16, block table."""
+        b = 0
+        for p, k in zip(self.n_prefix, self.n_keys):
+            b += p * self.hkv * self.d * 4 + 2 * self.n_new * self.hkv * self.d * 4
+            b += 2 * self.n_new * self.hq * self.d * 2 + 4 * ((k + 15) // 16)
+        return b
+
+
+def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 4, 8)):
+    n_layers, n_pref, n_new, hq, hkv, d = 18, 816, 51, 8, 1, 256
+    P = PagedLayers(c, 0xE3BD0000, [n_pref] * n_layers, n_new, hq, hkv, d, n_steps=10)
+    scale = 1.0 / math.sqrt(d)
+    best = None
+    sweep = {}
+    for sp in splits_list:
+        P.set_splits(sp)
+        ms, _ = c.time_graph(lambda st: P.attend(0, st, scale), steps, warmup)
+        sweep[sp] = ms * 1e3
+        if best is None or ms < best[1]:
+            best = (sp, ms)
+    P.set_splits(best[0])
+    attn_us = best[1] * 1e3
+    # K consecutive attention launches in one graph: the kernel's average duration
+    k_launch = 20
+
+    def attn_many(st):
+        for i in range(k_launch):
+            P.attend(i, st, scale)
+    ms_many, _ = c.time_graph(attn_many, max(2, steps // 4), 2)
+    attn_avg_us = ms_many * 1e3 / k_launch
+
+    step_counter = [0]
+
+    def one_step(st):
+        P.append(step_counter[0], st)
+        P.attend(step_counter[0], st, scale)
+    ms_step, _ = c.time_graph(one_step, steps, warmup)
+
+    # ten denoise steps (the whole config-1 workload) captured as one graph
+    def ten_steps(st):
+        for s in range(10):
+            P.append(s, st)
+            P.attend(s, st, scale)
+    ms_ten, _ = c.time_graph(ten_steps, max(2, steps // 4), 2)
+
+    # dependent per-layer launches (model-realistic ordering): 18 x (append, attention)
+    single = PagedLayers(c, 0xE3BD0000, [n_pref], n_new, hq, hkv, d, n_steps=1)
+    single.set_splits(8)
+    layers = [single] * n_layers  # same shapes; the graph holds 36 dependent launches
+
+    def per_layer(st):
+        for lp in layers:
+            lp.append(0, st)
+            lp.attend(0, st, scale)
+    ms_layer, _ = c.time_graph(per_layer, max(2, steps // 2), 2)
+
+    ab = P.attn_bytes()
+    return dict(
+        us_per_step=ms_step * 1e3,
+        us_per_step_10step_graph=ms_ten * 1e3 / 10,
+        us_per_step_dependent_layers=ms_layer * 1e3,
+        attn_us_single_launch=attn_us,
+        attn_us_avg_in_graph=attn_avg_us,
+        splits=best[0],
+        split_sweep_us=sweep,
+        attn_bytes_per_launch=ab,
+        attn_flops_per_launch=P.attn_flops(),
+        survey_bytes_per_step=P.survey_step_bytes(),
+    )
+
+
+def bench_cfg4(c: Ctx, steps, warmup):
+    from embkv import lib  # noqa: F401  (library loaded by Ctx)
+    res = {}
+    # L_b ~ U[300, 1200] from std::mt19937_64(0xE3BD0004): L_b = 300 + x % 901
+    g = MT64(0xE3BD0004)
+    lens_all = [300 + g.next() % 901 for _ in range(64)]
+    for B in (1, 8, 32, 64):
+        P = PagedLayers(c, 0xE3BD0004 + B, lens_all[:B], 51, 8, 1, 256, n_steps=2)
+        best = None
+        for sp in (1, 2, 4, 8):
+            if B >= 32 and sp > 2:
+                continue
+            P.set_splits(sp)
+            ms, _ = c.time_graph(lambda st: P.attend(0, st, 1 / 16), steps, warmup)
+            if best is None or ms < best[1]:
+                best = (sp, ms)
+        P.set_splits(best[0])
+
+        def one(st):
+            P.append(0, st)
+            P.attend(0, st, 1 / 16)
+        ms_all, _ = c.time_graph(one, steps, warmup)
+        ab = P.attn_bytes()
+        res[f"B{B}"] = dict(attn_us=best[1] * 1e3, append_plus_attn_us=ms_all * 1e3, splits=best[0],
+                            attn_gbs=ab / (best[1] * 1e-3) / 1e9,
+                            attn_hbm_frac=ab / (best[1] * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                            survey_bytes=P.survey_step_bytes(),
+                            survey_gbs=P.survey_step_bytes() / (ms_all * 1e-3) / 1e9,
+                            attn_tflops=P.attn_flops() / (best[1] * 1e-3) / 1e12,
+                            mean_prefix=float(np.mean(lens_all[:B])))
+        del P
+        c.torch.cuda.empty_cache()
+    return res
+
+
+def bench_cfg2(c: Ctx, steps, warmup):
+    """Prefix prefill + cache build: 18 layers x (append 816 tokens into pages, bidirectional
+    prefix attention 816 x 8 heads over 816 keys), one launch each for all layers."""
+    torch, emb = c.torch, c.emb
+    L, n, hq, hkv, d = 18, 816, 8, 1, 256
+    P = PagedLayers(c, 0xE3BD0001, [0] * L, n, hq, hkv, d, n_steps=1)
+    P.set_splits(1)
+
+    def one(st):
+        P.append(0, st)
+        P.attend(0, st, 1 / 16)
+    ms, _ = c.time_graph(one, steps, warmup)
+    ms_a, _ = c.time_graph(lambda st: P.attend(0, st, 1 / 16), steps, warmup)
+    fl = P.attn_flops()
+    return dict(us_per_prefill=ms * 1e3, attn_us=ms_a * 1e3, attn_tflops=fl / (ms_a * 1e-3) / 1e12,
+                mfma_frac=fl / (ms_a * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, flops=fl)
+
+
+def bench_cfg3(c: Ctx, steps, warmup, n_layers=30):
+    """LingBot-VA chunk step: 24 heads (MHA), head_dim 128, chunk 1560 tokens, 9-chunk window
+    (14040 slots).  Steady state: each step appends one chunk into the slots the evicted
+    oldest chunk held and attends over all 14040 keys; 30 dependent layers per step."""
+    torch, emb = c.torch, c.emb
+    H, d, C, W = 24, 128, 1560, 9
+    cap = C * W
+    pages = cap // 16 + (1 if cap % 16 else 0)
+    page_elems = H * 16 * d
+    base_k = c.synth(0xE3BD0002 + 1, cap * H * d)
+    base_v = c.synth(0xE3BD0002 + 2, cap * H * d)
+    q = c.synth(0xE3BD0002 + 3, C * H * d)
+    knew = c.synth(0xE3BD0002 + 4, C * H * d)
+    vnew = c.synth(0xE3BD0002 + 5, C * H * d)
+    pools = []
+    g = np.random.default_rng(3)
+    for l in range(n_layers):
+        bt = g.permutation(pages).astype(np.int32)
+        kp = torch.empty(pages * page_elems, dtype=torch.int16, device=c.dev)
+        vp = torch.empty_like(kp)
+        bt_d = c.i32(bt)
+        emb.kv_append(base_k, base_v, H * d, cap, c.i32(np.arange(cap)), bt_d, cap, kp, vp, H, d)
+        pools.append((kp, vp, bt_d))
+    out = torch.empty((C, H, d), dtype=torch.float32, device=c.dev)
+    cu = c.i32([0, C])
+    nk = c.i32([cap])
+    # the slot range the evicted oldest chunk held (chunk 0), reused by the new chunk
+    new_slots = c.i32(np.arange(C))
+    scale = 1 / math.sqrt(d)
+
+    def layer(l, st, append=True):
+        kp, vp, bt = pools[l]
+        if append:
+            emb.kv_append(knew, vnew, H * d, C, new_slots, bt, cap, kp, vp, H, d, stream=st)
+        emb.paged_attention(q=q, out=out, k_pool=kp, v_pool=vp, batch=1, hq=H, hkv=H, d=d, max_q=C,
+                            scale=scale, capacity=cap, cu_q=cu, n_keys=nk, block_tables=bt, bt_stride=pages,
+                            stream=st)
+
+    ms_step, _ = c.time_graph(lambda st: [layer(l, st) for l in range(n_layers)], max(2, steps // 4), 1)
+    ms_attn, _ = c.time_graph(lambda st: [layer(l, st, False) for l in range(n_layers)], max(2, steps // 4), 1)
+    fl_layer = 4.0 * C * H * cap * d
+    attn_layer_us = ms_attn * 1e3 / n_layers
+    del pools
+    torch.cuda.empty_cache()
+    return dict(ms_per_step=ms_step, attn_ms_per_step=ms_attn, attn_us_per_layer=attn_layer_us,
+                attn_tflops=fl_layer / (attn_layer_us * 1e-6) / 1e12,
+                mfma_frac=fl_layer / (attn_layer_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS,
+                flops_per_layer=fl_layer, layers=n_layers)
+
+
+class MT64:
+    """std::mt19937_64 (for drawing config-4 prefix lengths)."""
+
+    def __init__(self, seed):
+        self.mt = [0] * 312
+        self.mt[0] = seed & (2 ** 64 - 1)
+        for i in range(1, 312):
+            self.mt[i] = (6364136223846793005 * (self.mt[i - 1] ^ (self.mt[i - 1] >> 62)) + i) & (2 ** 64 - 1)
+        self.idx = 312
+
+    def next(self):
+        M = 2 ** 64 - 1
+        if self.idx >= 312:
+            for i in range(312):
+                x = (self.mt[i] & 0xFFFFFFFF80000000) | (self.mt[(i + 1) % 312] & 0x7FFFFFFF)
+                xa = x >> 1
+                if x & 1:
+                    xa ^= 0xB5026F5AA96619E9
+                self.mt[i] = self.mt[(i + 156) % 312] ^ xa
+            self.idx = 0
+        x = self.mt[self.idx]
+        self.idx += 1
+        x ^= (x >> 29) & 0x5555555555555555
+        x ^= (x << 17) & 0x71D67FFFEDA60000 & M
+        x ^= (x << 37) & 0xFFF7EEE000000000 & M
+        x ^= x >> 43
+        return x & M
+
+
+def cpu_baseline(target_s=10.0):
+    """Oracle fp32 restatement of the reference ggml CPU op order (pi05.cpp:414-418) over
+    config-1 layer problems on the host cores; whole denoise steps until ~target_s elapse."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    n_pref, n_new, hq, hkv, d = 816, 51, 8, 1, 256
+    nk = n_pref + n_new
+    k = oracle.bf16_to_f32(oracle.normal_bf16(0xE3BD0000 + 1, nk * hkv * d))
+    v = oracle.bf16_to_f32(oracle.normal_bf16(0xE3BD0000 + 2, nk * hkv * d))
+    q = oracle.bf16_to_f32(oracle.normal_bf16(0xE3BD0000 + 10, n_new * hq * d))
+
+    def step(th):
+        used = 0
+        for _ in range(18):
+            _, used = oracle.cpu_attention_f32(q, k, v, n_new, nk, hq, hkv, d, 1 / 16, th)
+        return used
+
+    res = {}
+    for th in sorted({threads, min(8, threads)}):
+        step(th)  # warm
+        t0 = time.perf_counter()
+        n = 0
+        used = th
+        while True:
+            used = step(th)
+            n += 1
+            if time.perf_counter() - t0 >= target_s / 2 or n >= 200:
+                break
+        res[th] = ((time.perf_counter() - t0) / n * 1e6, n, used)
+    th_main = max(res)
+    us, n, used = res[th_main]
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": us,
+        "unit": "us/denoise-step",
+        "cores": used,
+        "kind": "port",
+        "sample": (f"{n} config-1 denoise steps (18 layers of 51x8 queries over 867 keys, d=256) "
+                   f"with the oracle's fp32 ggml-order restatement on {used} OpenMP threads "
+                   f"(nproc={os.cpu_count()}, {cpu_model}); reference ggml b9016 is not available "
+                   f"offline; min(hw,8)={min(res)} threads: {res[min(res)][0]:.0f} us/step"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="cfg1,cfg2,cfg3,cfg4")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="cfg1_attn: only the headline kernel loop (profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the attention step has no multi-GPU path here; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    c = Ctx()
+    if args.only == "cfg1_attn":
+        P = PagedLayers(c, 0xE3BD0000, [816] * 18, 51, 8, 1, 256, n_steps=10)
+        P.set_splits(int(os.environ.get("EMB_SPLITS", "4")))
+        for i in range(args.warmup + args.steps):
+            P.attend(i, c.stream, 1 / 16)
+        c.torch.cuda.synchronize()
+        log("profile loop done")
+        return
+
+    cfgs = set(args.configs.split(","))
+    extra = {}
+    log("cfg1 ...")
+    r1 = bench_cfg1(c, args.steps, args.warmup)
+    extra["cfg1"] = r1
+    log("cfg1", json.dumps(r1))
+    if "cfg4" in cfgs:
+        log("cfg4 ...")
+        extra["cfg4"] = bench_cfg4(c, args.steps, args.warmup)
+        log("cfg4", json.dumps(extra["cfg4"]))
+    if "cfg2" in cfgs:
+        log("cfg2 ...")
+        extra["cfg2"] = bench_cfg2(c, args.steps, args.warmup)
+        log("cfg2", json.dumps(extra["cfg2"]))
+    if "cfg3" in cfgs:
+        log("cfg3 ...")
+        extra["cfg3"] = bench_cfg3(c, args.steps, args.warmup)
+        log("cfg3", json.dumps(extra["cfg3"]))
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        cpu = cpu_baseline()
+        log("cpu", json.dumps(cpu))
+
+    kern_us = r1["attn_us_avg_in_graph"]
+    achieved = r1["attn_bytes_per_launch"] / (kern_us * 1e-6) / 1e9
+    line = {
+        "metric": "us/denoise-step attention (pi0.5 action expert over cached prefix, 18 layers)",
+        "value": r1["us_per_step"],
+        "unit": "us/denoise-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r1["us_per_step"] / 1e3,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) bf16 from std::mt19937_64(0xE3BD0000+cfg), random-permuted page pool",
+        "config": {"workload": "BASELINE.json configs[0]: pi0.5 action-expert attention over an 816-token "
+                               "cached prefix, 18 layers, 51 queries x 8 heads / 1 kv head, head_dim 256, "
+                               "one denoise step = paged append of 51 new K/V + attention per layer, "
+                               "layers batched in one launch",
+                   "layers": 18, "prefix": 816, "queries": 51, "hq": 8, "hkv": 1, "head_dim": 256,
+                   "page_tokens": 16, "splits": r1["splits"]},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "kernel": "paged_attn_kernel<256,FULL>", "kernel_us": kern_us,
+                     "bytes_per_launch": r1["attn_bytes_per_launch"]},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

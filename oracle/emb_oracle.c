@@ -709,3 +709,94 @@ void orc_w8a16_gemm(const uint16_t *x, const int32_t *qweight, const uint16_t *s
     free(wT);
     free(sf);
 }
+
+/* ================= CPU baseline (timed by bench.py, not a checker) ================= */
+
+/* fp32 restatement of the reference's CPU op order for the action-expert
+ * attention (models/pi05.cpp:414-418: kq = mul_mat(K, Q) in F32,
+ * soft_max_ext(kq, mask = 0, scale), kqv = mul_mat(V, softmax)), threaded over
+ * (query, head) rows with OpenMP.  q [n_q][hq][d], k/v [n_k][hkv][d] already
+ * widened to f32, as ggml holds them. */
+__attribute__((target("avx2,fma"))) static void cpu_attn_row_avx2(const float *qr, const float *k,
+                                                                   const float *v, int64_t n_k,
+                                                                   int64_t hkv, int64_t kvh, int64_t d,
+                                                                   float scale, float *sc, float *o) {
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < n_k; ++j) {
+        const float *kr = k + (j * hkv + kvh) * d;
+        float dot = 0.0f;
+#pragma omp simd reduction(+ : dot)
+        for (int64_t x = 0; x < d; ++x) dot += qr[x] * kr[x];
+        sc[j] = dot * scale;
+        if (sc[j] > mx) mx = sc[j];
+    }
+    float sum = 0.0f;
+    for (int64_t j = 0; j < n_k; ++j) {
+        sc[j] = expf(sc[j] - mx);
+        sum += sc[j];
+    }
+    for (int64_t x = 0; x < d; ++x) o[x] = 0.0f;
+    for (int64_t j = 0; j < n_k; ++j) {
+        const float *vr = v + (j * hkv + kvh) * d;
+        const float p = sc[j];
+#pragma omp simd
+        for (int64_t x = 0; x < d; ++x) o[x] += p * vr[x];
+    }
+    const float inv = 1.0f / sum;
+    for (int64_t x = 0; x < d; ++x) o[x] *= inv;
+}
+
+static void cpu_attn_row_generic(const float *qr, const float *k, const float *v, int64_t n_k,
+                                 int64_t hkv, int64_t kvh, int64_t d, float scale, float *sc, float *o) {
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < n_k; ++j) {
+        const float *kr = k + (j * hkv + kvh) * d;
+        float dot = 0.0f;
+        for (int64_t x = 0; x < d; ++x) dot += qr[x] * kr[x];
+        sc[j] = dot * scale;
+        if (sc[j] > mx) mx = sc[j];
+    }
+    float sum = 0.0f;
+    for (int64_t j = 0; j < n_k; ++j) {
+        sc[j] = expf(sc[j] - mx);
+        sum += sc[j];
+    }
+    for (int64_t x = 0; x < d; ++x) o[x] = 0.0f;
+    for (int64_t j = 0; j < n_k; ++j) {
+        const float *vr = v + (j * hkv + kvh) * d;
+        for (int64_t x = 0; x < d; ++x) o[x] += sc[j] * vr[x];
+    }
+    for (int64_t x = 0; x < d; ++x) o[x] /= sum;
+}
+
+int orc_cpu_attention_f32(const float *q, const float *k, const float *v, int64_t n_q, int64_t n_k,
+                          int64_t hq, int64_t hkv, int64_t d, float scale, int threads, float *out) {
+    const int avx2 = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+    const int64_t G = hq / hkv;
+    int used = 1;
+#ifdef _OPENMP
+    int nt = threads > 0 ? threads : omp_get_max_threads();
+#pragma omp parallel num_threads(nt)
+#else
+    (void)threads;
+#endif
+    {
+        float *sc = (float *)malloc(sizeof(float) * (size_t)(n_k + 1));
+#ifdef _OPENMP
+#pragma omp single
+        used = omp_get_num_threads();
+#pragma omp for schedule(static)
+#endif
+        for (int64_t w = 0; w < n_q * hq; ++w) {
+            const int64_t i = w / hq, h = w % hq;
+            const float *qr = q + (i * hq + h) * d;
+            float *o = out + (i * hq + h) * d;
+            if (avx2)
+                cpu_attn_row_avx2(qr, k, v, n_k, hkv, h / G, d, scale, sc, o);
+            else
+                cpu_attn_row_generic(qr, k, v, n_k, hkv, h / G, d, scale, sc, o);
+        }
+        free(sc);
+    }
+    return used;
+}

@@ -128,6 +128,11 @@ void orc_gqa_attention_bf16(const uint16_t *q, const uint16_t *k, const uint16_t
                             int64_t window, int64_t q_pos0, const int64_t *rows, int64_t n_rows,
                             int threads, float *out);
 
+/* CPU baseline (bench.py cpu_baseline leg): f32 ggml op order, OpenMP threads.
+ * Returns the number of threads used. */
+int orc_cpu_attention_f32(const float *q, const float *k, const float *v, int64_t n_q, int64_t n_k,
+                          int64_t hq, int64_t hkv, int64_t d, float scale, int threads, float *out);
+
 /* ---------------- W8 Marlin (kernels/cosmos3/cosmos3_w8_marlin_cuda.cu:50-88) ---------------- */
 int64_t orc_marlin_dst_byte(int64_t k, int64_t n, int64_t out_features);
 int64_t orc_marlin_scale_index(int64_t n);

@@ -69,6 +69,8 @@ _SIGS = {
     "orc_gqa_attention_bf16": (None, [u16p, u16p, u16p, C.c_int64, C.c_int64, C.c_int64,
                                       C.c_int64, C.c_int64, C.c_float, u8p, f32p, C.c_int64,
                                       C.c_int64, C.c_int64, i64p, C.c_int64, C.c_int, f32p]),
+    "orc_cpu_attention_f32": (C.c_int, [f32p, f32p, f32p, C.c_int64, C.c_int64, C.c_int64,
+                                        C.c_int64, C.c_int64, C.c_float, C.c_int, f32p]),
     "orc_marlin_dst_byte": (C.c_int64, [C.c_int64, C.c_int64, C.c_int64]),
     "orc_marlin_scale_index": (C.c_int64, [C.c_int64]),
     "orc_marlin_pack_w8": (None, [i8p, C.c_int64, C.c_int64, i32p]),
@@ -291,6 +293,16 @@ def gqa_attention(q, k, v, n_q, n_k, hq, hkv, d, scale, allow=None, add=None, ch
                                  P(al, u8p), P(ad, f32p), chunk, window, q_pos0, P(r, i64p),
                                  0 if r is None else len(r), threads, P(out, f32p))
     return out.reshape(n_q, hq, d)
+
+
+def cpu_attention_f32(q, k, v, n_q, n_k, hq, hkv, d, scale, threads=0):
+    """CPU baseline: f32 arrays in, (out f32 [n_q][hq][d], threads used) back."""
+    out = np.zeros(n_q * hq * d, np.float32)
+    used = lib().orc_cpu_attention_f32(P(np.ascontiguousarray(q, np.float32), f32p),
+                                       P(np.ascontiguousarray(k, np.float32), f32p),
+                                       P(np.ascontiguousarray(v, np.float32), f32p), n_q, n_k, hq,
+                                       hkv, d, scale, threads, P(out, f32p))
+    return out.reshape(n_q, hq, d), used
 
 
 # ---------------- W8 ----------------
