@@ -11,20 +11,30 @@
 // Work decomposition.  A workgroup of 4 waves owns 128 query rows of one
 // (sequence, kv head); a row is (token, q head of the GQA group), so all query
 // heads that share a kv head also share every K/V tile the workgroup stages in
-// LDS.  Each wave owns 32 rows.  Keys stream in tiles of 32 (two pages).
+// LDS.  Each wave owns 32 rows.  Keys stream in tiles of KT = 64 keys (32 at
+// head_dim 256).
+//
+// Pipeline.  K/V tiles are double-buffered in LDS.  While a wave computes tile
+// t from one buffer, the global loads of tile t+1 are already in flight into
+// registers, and the block-table entries of tile t+2 are being fetched; after
+// the compute the registers are converted and written to the other buffer and
+// one barrier per tile hands it over.  The page ids of a tile are the same for
+// every thread of the workgroup, so they come through scalar loads.
 //
 // Per wave and key tile the math is done transposed, with MFMA 32x32x16:
 //   S^T[32 keys x 32 rows] = K[keys x D] . Q^T       (bf16 x bf16 -> f32)
 //   O^T[D x 32 rows]      += V^T[D x keys] . P^T      (f16 x f16 -> f32)
-// so that lane l owns query row l%32: its 16 scores and its D/2 output
+// so that lane l owns query row l%32: its scores and its D/2 output
 // accumulators all belong to the same row, the row max needs one cross-lane
 // step (lanes l and l^32), and rescaling needs no shuffles.  P and V go through
 // f16 rather than bf16 because P in bf16 (8 significant bits) alone would put
 // the mean relative error near 1.6e-3; f16 keeps it near 2e-4.  V is converted
 // bf16 -> f16 while it is staged in LDS (exact for |v| in [2^-14, 65504]).
 //
-// The online softmax works in log2 units and rescales the accumulators only
-// when a row max grows by more than 2^8, so most tiles skip the rescale.
+// The online softmax keeps the running max in raw score units and rescales
+// the accumulators only when some row's max grows by more than 2^8 in the
+// exponent; the decision is taken per wave (ballot), so the rescale is a
+// uniform branch that most tiles skip.
 //
 // Split-K: with splits > 1 each workgroup handles one key range and writes
 // unnormalised partials (O, m, l) that attn_merge_kernel combines.
@@ -39,7 +49,6 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -48,9 +57,25 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int WAVES = 4;
 constexpr int ROWS_PER_WAVE = 32;
 constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
-constexpr int KT = 32;          // keys per tile (two pages)
 constexpr float RESCALE_TH = 8.0f;  // log2 units
 constexpr float LOG2E = 1.4426950408889634f;
+
+template <int D>
+struct Geo {
+    // keys per tile: four pages, two at D = 256 where the accumulators and the
+    // query fragment already hold 192 registers a lane
+    static constexpr int KT = D >= 256 ? 32 : 64;
+    static constexpr int KB = KT / 32;             // 32-key MFMA blocks per tile
+    static constexpr int PAGES = KT / 16;
+    static constexpr int CH = D / 8;               // 16-byte chunks per key row
+    static constexpr int KS = D + 8;               // bf16 elements per staged K row
+    static constexpr int VS = KT + 8;              // f16 elements per staged V^T row
+    static constexpr int KPT = KT * CH / 256;      // K chunks per thread per tile
+    static constexpr int VPT = D * KT / 8 / 256;   // V chunks per thread per tile
+    static constexpr int STAGE = KT * KS + D * VS; // uint16 elements per LDS stage
+    static constexpr int MIN_WG = D >= 256 ? 1 : 2;
+    static_assert(KPT >= 1 && VPT >= 1, "tile too small for 256 threads");
+};
 
 struct KParams {
     const void *q;
@@ -71,7 +96,9 @@ struct KParams {
     int32_t row_tiles;
     int32_t splits;
     int32_t total_wg;
-    float scale_log2;
+    float c_log2;     // scale * log2(e)
+    float th_raw;     // RESCALE_TH / c_log2
+    float inv_scale;  // 1 / scale (additive masks are added in raw score units)
     int32_t chunk, window;
     const void *mask;
     int64_t mask_q_stride, mask_b_stride;
@@ -97,91 +124,155 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
     return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
 }
 
-template <int D>
-struct Smem {
-    static constexpr int KS_STRIDE = D + 8;    // bf16 elements per staged key row
-    static constexpr int VS_STRIDE = KT + 8;   // f16 elements per staged dim row
-    uint16_t ks[KT * KS_STRIDE];
-    uint16_t vs[D * VS_STRIDE];
-};
-
-template <bool VALID>
-__device__ __forceinline__ int32_t key_slot(const KParams &p, const int32_t *valid_b, int32_t j, int32_t nk) {
-    if (j >= nk) return -2;  // beyond the key list: zero row, masked
-    if (!VALID) return j;
-    return valid_b[j];
+// Page of logical slot `slot` of sequence b (identity map without a table).
+__device__ __forceinline__ int32_t page_of(const int32_t *bt_b, int32_t slot) {
+    return bt_b ? bt_b[slot >> 4] : (slot >> 4);
 }
 
-__device__ __forceinline__ int64_t page_of(const int32_t *bt_b, int32_t slot) {
-    return bt_b ? (int64_t)bt_b[slot >> 4] : (int64_t)(slot >> 4);
-}
-
-// Stages keys [k0, k0+32) into LDS: K rows as bf16, V as f16 in the transposed,
-// key-permuted layout the PV MFMA reads (within a page, key t sits at position
-// t with bits 2 and 3 swapped).
+// Global-to-register staging of one K/V tile.
 template <int D, bool VALID>
-__device__ __forceinline__ void stage_tile(const KParams &p, Smem<D> &sm, const int32_t *valid_b,
-                                           const int32_t *bt_b, int32_t k0, int32_t nk, int32_t kvh) {
-    constexpr int CH = D / 8;  // 16-byte chunks per key row
-    const int tid = threadIdx.x;
-    // K: KT keys x CH chunks
+struct Loader {
+    using G = Geo<D>;
+    u32x4 k[G::KPT];
+    u32x4 v[G::VPT];
+
+    // Keys of the tile are k0 + [0, KT).  Without a valid-slot list, key j is
+    // logical slot j, so every 8-key group of V is contiguous inside one page
+    // and pages[] (the tile's KT/16 page ids, uniform over the workgroup) is
+    // all that is needed.
+    __device__ __forceinline__ void issue_direct(const KParams &p, const int32_t (&pages)[G::PAGES], int32_t k0,
+                                                 int32_t nk, int32_t kvh) {
+        const int tid = threadIdx.x;
+        nk = min(nk, p.capacity);  // slots at or past the capacity are zero rows
 #pragma unroll
-    for (int it = 0; it < (KT * CH) / 256; ++it) {
-        const int c = tid + it * 256;
-        const int key = c / CH, dc = c % CH;
-        const int32_t slot = key_slot<VALID>(p, valid_b, k0 + key, nk);
-        u32x4 w = {0u, 0u, 0u, 0u};
-        if (slot >= 0 && slot < p.capacity) {
-            const int64_t page = page_of(bt_b, slot);
-            if (page >= 0)
-                w = *reinterpret_cast<const u32x4 *>(p.k_pool + ((page * p.hkv + kvh) * 16 + (slot & 15)) * D + dc * 8);
+        for (int i = 0; i < G::KPT; ++i) {
+            const int c = tid + i * 256;
+            const int key = c / G::CH, dc = c % G::CH;
+            const int32_t j = k0 + key;
+            const int32_t page = pages[key >> 4];
+            k[i] = u32x4{0u, 0u, 0u, 0u};
+            if (j < nk && page >= 0)
+                k[i] = *reinterpret_cast<const u32x4 *>(p.k_pool + (((int64_t)page * p.hkv + kvh) * 16 + (j & 15)) * D +
+                                                        dc * 8);
         }
-        *reinterpret_cast<u32x4 *>(&sm.ks[key * Smem<D>::KS_STRIDE + dc * 8]) = w;
-    }
-    // V: 2 pages x D dims x 2 halves of 8 keys
 #pragma unroll
-    for (int it = 0; it < (4 * D) / 256; ++it) {
-        const int c = tid + it * 256;
-        const int pg = c / (2 * D);
-        const int rem = c % (2 * D);
-        const int d = rem >> 1, half = rem & 1;
-        const int jb = k0 + pg * 16 + half * 8;  // first key of these 8
-        u32x4 w = {0u, 0u, 0u, 0u};
-        const int32_t s0 = key_slot<VALID>(p, valid_b, jb, nk);
-        bool fast = s0 >= 0 && (s0 & 7) == 0 && s0 + 7 < p.capacity && jb + 7 < nk;
-        if (VALID && fast) {
+        for (int i = 0; i < G::VPT; ++i) {
+            const int c = tid + i * 256;
+            const int pg = c / (2 * D);
+            const int rem = c % (2 * D);
+            const int d = rem >> 1, half = rem & 1;
+            const int32_t jb = k0 + pg * 16 + half * 8;
+            const int32_t page = pages[pg];
+            v[i] = u32x4{0u, 0u, 0u, 0u};
+            if (jb < nk && page >= 0) {
+                v[i] = *reinterpret_cast<const u32x4 *>(p.v_pool + (((int64_t)page * p.hkv + kvh) * D + d) * 16 +
+                                                        half * 8);
+                if (jb + 8 > nk) {  // group straddles the key count: zero the tail keys
 #pragma unroll
-            for (int e = 1; e < 8; ++e) fast = fast && valid_b[jb + e] == s0 + e;
-        }
-        if (fast) {
-            const int64_t page = page_of(bt_b, s0);
-            if (page >= 0)
-                w = *reinterpret_cast<const u32x4 *>(p.v_pool + ((page * p.hkv + kvh) * D + d) * 16 + (s0 & 15));
-        } else {
-            uint32_t hv[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int32_t s = key_slot<VALID>(p, valid_b, jb + e, nk);
-                hv[e] = 0u;
-                if (s >= 0 && s < p.capacity) {
-                    const int64_t page = page_of(bt_b, s);
-                    if (page >= 0) hv[e] = p.v_pool[((page * p.hkv + kvh) * D + d) * 16 + (s & 15)];
+                    for (int e = 0; e < 8; ++e)
+                        if (jb + e >= nk) v[i][e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
                 }
             }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w[e] = hv[2 * e] | (hv[2 * e + 1] << 16);
         }
-        u32x2 lo = {bf16x2_to_f16x2(w[0]), bf16x2_to_f16x2(w[1])};  // keys +0..3
-        u32x2 hi = {bf16x2_to_f16x2(w[2]), bf16x2_to_f16x2(w[3])};  // keys +4..7
-        uint16_t *row = &sm.vs[d * Smem<D>::VS_STRIDE + pg * 16];
-        *reinterpret_cast<u32x2 *>(row + half * 4) = lo;
-        *reinterpret_cast<u32x2 *>(row + 8 + half * 4) = hi;
+    }
+
+    // With a valid-slot list key j is logical slot valid[j] (a negative or
+    // out-of-range slot is a zero row).
+    __device__ __forceinline__ void issue_valid(const KParams &p, const int32_t *valid_b, const int32_t *bt_b,
+                                                int32_t k0, int32_t nk, int32_t kvh) {
+        const int tid = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < G::KPT; ++i) {
+            const int c = tid + i * 256;
+            const int key = c / G::CH, dc = c % G::CH;
+            const int32_t j = k0 + key;
+            k[i] = u32x4{0u, 0u, 0u, 0u};
+            const int32_t s = j < nk ? valid_b[j] : -1;
+            if (s >= 0 && s < p.capacity) {
+                const int32_t page = page_of(bt_b, s);
+                if (page >= 0)
+                    k[i] = *reinterpret_cast<const u32x4 *>(
+                        p.k_pool + (((int64_t)page * p.hkv + kvh) * 16 + (s & 15)) * D + dc * 8);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < G::VPT; ++i) {
+            const int c = tid + i * 256;
+            const int pg = c / (2 * D);
+            const int rem = c % (2 * D);
+            const int d = rem >> 1, half = rem & 1;
+            const int32_t jb = k0 + pg * 16 + half * 8;
+            int32_t s[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] = jb + e < nk ? valid_b[jb + e] : -1;
+            bool run = s[0] >= 0 && (s[0] & 7) == 0 && s[0] + 7 < p.capacity;
+#pragma unroll
+            for (int e = 1; e < 8; ++e) run = run && s[e] == s[0] + e;
+            u32x4 w = {0u, 0u, 0u, 0u};
+            if (run) {
+                const int32_t page = page_of(bt_b, s[0]);
+                if (page >= 0)
+                    w = *reinterpret_cast<const u32x4 *>(p.v_pool + (((int64_t)page * p.hkv + kvh) * D + d) * 16 +
+                                                         (s[0] & 15));
+            } else {
+                uint32_t hv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    hv[e] = 0u;
+                    if (s[e] >= 0 && s[e] < p.capacity) {
+                        const int32_t page = page_of(bt_b, s[e]);
+                        if (page >= 0) hv[e] = p.v_pool[(((int64_t)page * p.hkv + kvh) * D + d) * 16 + (s[e] & 15)];
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = hv[2 * e] | (hv[2 * e + 1] << 16);
+            }
+            v[i] = w;
+        }
+    }
+
+    // Registers -> LDS stage: K rows as bf16; V transposed to [d][key] in f16
+    // with the key permutation the PV MFMA reads (within a 16-key page, key t
+    // sits at position t with bits 2 and 3 swapped).
+    __device__ __forceinline__ void store(uint16_t *stage) const {
+        const int tid = threadIdx.x;
+        uint16_t *ks = stage;
+        uint16_t *vs = stage + G::KT * G::KS;
+#pragma unroll
+        for (int i = 0; i < G::KPT; ++i) {
+            const int c = tid + i * 256;
+            const int key = c / G::CH, dc = c % G::CH;
+            *reinterpret_cast<u32x4 *>(&ks[key * G::KS + dc * 8]) = k[i];
+        }
+#pragma unroll
+        for (int i = 0; i < G::VPT; ++i) {
+            const int c = tid + i * 256;
+            const int pg = c / (2 * D);
+            const int rem = c % (2 * D);
+            const int d = rem >> 1, half = rem & 1;
+            const u32x2 lo = {bf16x2_to_f16x2(v[i][0]), bf16x2_to_f16x2(v[i][1])};  // keys +0..3
+            const u32x2 hi = {bf16x2_to_f16x2(v[i][2]), bf16x2_to_f16x2(v[i][3])};  // keys +4..7
+            uint16_t *row = &vs[d * G::VS + pg * 16];
+            *reinterpret_cast<u32x2 *>(row + half * 4) = lo;
+            *reinterpret_cast<u32x2 *>(row + 8 + half * 4) = hi;
+        }
+    }
+};
+
+template <int D>
+__device__ __forceinline__ void load_pages(const int32_t *bt_b, int32_t k0, int32_t nk, int32_t capacity,
+                                           int32_t (&pages)[Geo<D>::PAGES]) {
+#pragma unroll
+    for (int pg = 0; pg < Geo<D>::PAGES; ++pg) {
+        const int32_t j = k0 + pg * 16;
+        pages[pg] = (j < nk && j < capacity) ? page_of(bt_b, j) : -1;
     }
 }
 
 template <int D, int MASK, bool VALID, bool QF32>
-__global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void paged_attn_kernel(KParams p) {
-    __shared__ Smem<D> sm;
+__global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams p) {
+    using G = Geo<D>;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * G::STAGE];
 
     // XCD-aware order: hardware ids go round-robin over the 8 XCDs, so logical
     // work ids are handed out in contiguous runs per XCD, keeping the row tiles
@@ -243,14 +334,14 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void paged_attn_kernel(KPara
     }
 
     // Key range of this workgroup: mask bounds, then this split's share.
+    const int32_t last_row = min(row0 + ROWS_PER_WG, rows) - 1;
+    const int32_t qp_min = qpos0 + row0 / p.G, qp_max = qpos0 + last_row / p.G;
     int32_t k_lo = 0, k_hi = nk;
     if (MASK == EMB_MASK_CHUNK) {
-        const int32_t last_row = min(row0 + ROWS_PER_WG, rows) - 1;
-        const int32_t qp_min = qpos0 + row0 / p.G, qp_max = qpos0 + last_row / p.G;
         k_hi = min(nk, (qp_max / p.chunk + 1) * p.chunk);
         if (p.window >= 0) k_lo = max(0, (qp_min / p.chunk - p.window) * p.chunk);
     }
-    int32_t t_lo = k_lo / KT, t_hi = (max(k_hi, k_lo) + KT - 1) / KT;
+    int32_t t_lo = k_lo / G::KT, t_hi = (max(k_hi, k_lo) + G::KT - 1) / G::KT;
     if (p.splits > 1) {
         const int32_t nt = t_hi - t_lo;
         const int32_t per = (nt + p.splits - 1) / p.splits;
@@ -258,86 +349,142 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void paged_attn_kernel(KPara
         t_hi = min(t_hi, a + per);
         t_lo = min(a, t_hi);
     }
+    // Keys every row of the workgroup sees under a chunk mask (no per-key test needed there).
+    int32_t full_lo = 0, full_hi = nk;
+    if (MASK == EMB_MASK_CHUNK) {
+        full_hi = min(nk, (qp_min / p.chunk + 1) * p.chunk);
+        full_lo = p.window >= 0 ? max(0, (qp_max / p.chunk - p.window) * p.chunk) : 0;
+    }
 
     f32x16 acc_o[D / 32];
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) acc_o[i] = f32x16{};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    for (int32_t t = t_lo; t < t_hi; ++t) {
-        const int32_t k0 = t * KT;
+    Loader<D, VALID> ld;
+    int32_t pages_n[G::PAGES], pages_nn[G::PAGES];  // tiles t+1 and t+2
+    if (t_lo < t_hi) {
+        if (VALID) {
+            ld.issue_valid(p, valid_b, bt_b, t_lo * G::KT, nk, kvh);
+        } else {
+            int32_t pg0[G::PAGES];
+            load_pages<D>(bt_b, t_lo * G::KT, nk, p.capacity, pg0);
+            ld.issue_direct(p, pg0, t_lo * G::KT, nk, kvh);
+            load_pages<D>(bt_b, (t_lo + 1) * G::KT, nk, p.capacity, pages_n);
+        }
+        ld.store(smem);
         __syncthreads();
-        stage_tile<D, VALID>(p, sm, valid_b, bt_b, k0, nk, kvh);
-        __syncthreads();
+    }
 
-        // S^T = K Q^T : lane holds keys (r/4)*8 + lhi*4 + r%4 of row lrow.
-        f32x16 s = f32x16{};
-#pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-            const u32x4 kw =
-                *reinterpret_cast<const u32x4 *>(&sm.ks[lrow * Smem<D>::KS_STRIDE + kk * 16 + lhi * 8]);
-            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kw), qf[kk], s, 0, 0, 0);
+    for (int32_t t = t_lo; t < t_hi; ++t) {
+        const int32_t k0 = t * G::KT;
+        const bool more = t + 1 < t_hi;
+        const uint16_t *cur = smem + ((t - t_lo) & 1) * G::STAGE;
+        uint16_t *nxt = smem + ((t - t_lo + 1) & 1) * G::STAGE;
+
+        // (1) loads of tile t+1 in flight during the compute of tile t
+        if (more) {
+            if (VALID) {
+                ld.issue_valid(p, valid_b, bt_b, k0 + G::KT, nk, kvh);
+            } else {
+                ld.issue_direct(p, pages_n, k0 + G::KT, nk, kvh);
+                load_pages<D>(bt_b, k0 + 2 * G::KT, nk, p.capacity, pages_nn);
+            }
         }
 
-        // scale, mask, tile max
-        float mt = -INFINITY;
-        const bool tile_full = (MASK == EMB_MASK_FULL) && (k0 + KT <= nk);
+        // (2) S^T = K Q^T : in block kb, lane holds keys kb*32 + (r/4)*8 + lhi*4 + r%4 of row lrow.
+        const uint16_t *ks = cur;
+        const uint16_t *vs = cur + G::KT * G::KS;
+        f32x16 s[G::KB];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int32_t j = k0 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-            float x = s[r] * p.scale_log2;
-            if (!tile_full) {
-                bool vis = row_ok && j < nk;
-                if (MASK == EMB_MASK_CHUNK) {
-                    const int32_t qc = qpos / p.chunk, kc = j / p.chunk;
-                    vis = vis && kc <= qc && (p.window < 0 || qc - kc <= p.window);
-                } else if (MASK == EMB_MASK_TOKEN) {
-                    vis = vis && reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
-                                                                          (int64_t)tok * p.mask_q_stride + j] != 0;
-                } else if (MASK == EMB_MASK_ADD) {
-                    if (vis)
-                        x += LOG2E * reinterpret_cast<const float *>(p.mask)[(int64_t)b * p.mask_b_stride +
-                                                                             (int64_t)tok * p.mask_q_stride + j];
-                } else if (MASK == EMB_MASK_BLOCKMAP) {
-                    vis = vis && p.bmap[(int64_t)b * p.bmap_b_stride + (int64_t)(tok / p.bsize) * p.bmap_cols +
-                                        j / p.bsize] != 0;
-                    if (vis && p.mask)
-                        vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
-                                                                        (int64_t)tok * p.mask_q_stride + j] != 0;
-                }
-                if (!vis) x = -INFINITY;
+        for (int kb = 0; kb < G::KB; ++kb) {
+            s[kb] = f32x16{};
+#pragma unroll
+            for (int kk = 0; kk < D / 16; ++kk) {
+                const u32x4 kw = *reinterpret_cast<const u32x4 *>(&ks[(kb * 32 + lrow) * G::KS + kk * 16 + lhi * 8]);
+                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kw), qf[kk], s[kb], 0, 0, 0);
             }
-            s[r] = x;
-            mt = fmaxf(mt, x);
+        }
+
+        // (3) mask (raw score units), tile max
+        bool tile_full = k0 + G::KT <= nk;
+        if (MASK == EMB_MASK_CHUNK) tile_full = tile_full && k0 >= full_lo && k0 + G::KT <= full_hi;
+        if (MASK == EMB_MASK_TOKEN || MASK == EMB_MASK_ADD || MASK == EMB_MASK_BLOCKMAP) tile_full = false;
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < G::KB; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float x = s[kb][r];
+                if (!tile_full) {
+                    const int32_t j = k0 + kb * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                    bool vis = row_ok && j < nk;
+                    if (MASK == EMB_MASK_CHUNK) {
+                        const int32_t qc = qpos / p.chunk, kc = j / p.chunk;
+                        vis = vis && kc <= qc && (p.window < 0 || qc - kc <= p.window);
+                    } else if (MASK == EMB_MASK_TOKEN) {
+                        vis = vis && reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                              (int64_t)tok * p.mask_q_stride + j] != 0;
+                    } else if (MASK == EMB_MASK_ADD) {
+                        if (vis)
+                            x += p.inv_scale * reinterpret_cast<const float *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                                      (int64_t)tok * p.mask_q_stride + j];
+                    } else if (MASK == EMB_MASK_BLOCKMAP) {
+                        vis = vis && p.bmap[(int64_t)b * p.bmap_b_stride + (int64_t)(tok / p.bsize) * p.bmap_cols +
+                                            j / p.bsize] != 0;
+                        if (vis && p.mask)
+                            vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                            (int64_t)tok * p.mask_q_stride + j] != 0;
+                    }
+                    if (!vis) x = -INFINITY;
+                    s[kb][r] = x;
+                }
+                mt = fmaxf(mt, x);
+            }
         }
         mt = fmaxf(mt, __shfl_xor(mt, 32));
-        if (mt > m_run + RESCALE_TH) {
-            const float alpha = __builtin_amdgcn_exp2f(m_run - mt);  // m_run = -inf -> 0
+        // (4) wave-uniform lazy rescale
+        if (__builtin_amdgcn_ballot_w64(mt > m_run + p.th_raw) != 0) {
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
 #pragma unroll
             for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
             l_run *= alpha;
-            m_run = mt;
+            m_run = m_new;
         }
-        const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-        f16x8 pf[2];
+        const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * p.c_log2;
+        f16x8 pf[G::KB][2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float e = __builtin_amdgcn_exp2f(s[r] - m_use);
-            l_run += e;
-            pf[r >> 3][r & 7] = (_Float16)e;
-        }
+        for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], p.c_log2, neg_mc));
+                l_run += e;
+                pf[kb][r >> 3][r & 7] = (_Float16)e;
+            }
 
-        // O^T += V^T P^T, one 16-key page per MFMA step.
+        // (5) O^T += V^T P^T, one 16-key page per MFMA step.
 #pragma unroll
-        for (int pg = 0; pg < 2; ++pg) {
+        for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt) {
-                const u32x4 vw = *reinterpret_cast<const u32x4 *>(
-                    &sm.vs[(dt * 32 + lrow) * Smem<D>::VS_STRIDE + pg * 16 + lhi * 8]);
-                acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vw), pf[pg],
-                                                                  acc_o[dt], 0, 0, 0);
+            for (int pg = 0; pg < 2; ++pg)
+#pragma unroll
+                for (int dt = 0; dt < D / 32; ++dt) {
+                    const u32x4 vw = *reinterpret_cast<const u32x4 *>(
+                        &vs[(dt * 32 + lrow) * G::VS + kb * 32 + pg * 16 + lhi * 8]);
+                    acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vw), pf[kb][pg],
+                                                                      acc_o[dt], 0, 0, 0);
+                }
+
+        // (6) hand tile t+1 over through the other LDS stage
+        if (more) {
+            ld.store(nxt);
+            if (!VALID) {
+#pragma unroll
+                for (int i = 0; i < G::PAGES; ++i) pages_n[i] = pages_nn[i];
             }
         }
+        __syncthreads();
     }
 
     l_run += __shfl_xor(l_run, 32);
@@ -355,7 +502,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void paged_attn_kernel(KPara
                 *reinterpret_cast<f32x4 *>(wo + dt * 32 + j * 8 + lhi * 4) = v;
             }
         if (lhi == 0) {
-            p.ws_ml[rowi * 2] = m_run;
+            p.ws_ml[rowi * 2] = m_run == -INFINITY ? -INFINITY : m_run * p.c_log2;
             p.ws_ml[rowi * 2 + 1] = l_run;
         }
         return;
@@ -373,7 +520,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void paged_attn_kernel(KPara
         }
 }
 
-// Combines split partials: m = max m_s, l = sum l_s 2^(m_s - m),
+// Combines split partials (m in log2 units): m = max m_s, l = sum l_s 2^(m_s - m),
 // out = sum O_s 2^(m_s - m) / l.  One thread per (row, 4 dims).
 template <int D>
 __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
@@ -457,6 +604,7 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     EMB_CHECK_ARG(a->capacity > 0, "capacity must be positive");
     EMB_CHECK_ARG(!a->valid_slots || a->valid_stride >= 0, "bad valid_stride");
     EMB_CHECK_ARG(!a->block_tables || a->bt_stride > 0, "bad bt_stride");
+    EMB_CHECK_ARG(a->scale > 0.0f && std::isfinite(a->scale), "scale must be positive and finite");
     const int64_t esz = a->q_is_f32 ? 4 : 2;
     EMB_CHECK_ARG(a->q_stride >= (int64_t)a->hq * a->head_dim && (a->q_stride * esz) % 16 == 0,
                   "q_stride must cover a token and keep 16-byte alignment");
@@ -498,7 +646,9 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     const int64_t total = (int64_t)a->batch * a->hkv * splits * kp.row_tiles;
     EMB_CHECK_ARG(total < INT_MAX / 2, "grid too large");
     kp.total_wg = (int32_t)total;
-    kp.scale_log2 = a->scale * LOG2E;
+    kp.c_log2 = a->scale * LOG2E;
+    kp.th_raw = RESCALE_TH / kp.c_log2;
+    kp.inv_scale = 1.0f / a->scale;
     kp.chunk = a->chunk;
     kp.window = a->window;
     kp.mask = a->mask;
