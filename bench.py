@@ -295,7 +295,7 @@ def bench_cfg2(c: Ctx, steps, warmup):
                 mfma_frac=fl / (ms_a * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, flops=fl)
 
 
-def bench_cfg3(c: Ctx, steps, warmup, n_layers=30):
+def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
     """LingBot-VA chunk step: 24 heads (MHA), head_dim 128, chunk 1560 tokens, 9-chunk window
     (14040 slots).  Steady state: each step appends one chunk into the slots the evicted
     oldest chunk held and attends over all 14040 keys; 30 dependent layers per step."""
@@ -333,6 +333,11 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30):
                             scale=scale, capacity=cap, cu_q=cu, n_keys=nk, block_tables=bt, bt_stride=pages,
                             stream=st)
 
+    if eager_only:  # profiling: plain launches of the attention kernel
+        for i in range(warmup + steps):
+            layer(i % n_layers, c.stream, False)
+        torch.cuda.synchronize()
+        return {}
     ms_step, _ = c.time_graph(lambda st: [layer(l, st) for l in range(n_layers)], max(2, steps // 4), 1)
     ms_attn, _ = c.time_graph(lambda st: [layer(l, st, False) for l in range(n_layers)], max(2, steps // 4), 1)
     fl_layer = 4.0 * C * H * cap * d
@@ -445,10 +450,14 @@ def main():
     c = Ctx()
     if args.only == "cfg1_attn":
         P = PagedLayers(c, 0xE3BD0000, [816] * 18, 51, 8, 1, 256, n_steps=10)
-        P.set_splits(int(os.environ.get("EMB_SPLITS", "4")))
+        P.set_splits(int(os.environ.get("EMB_SPLITS", "2")))
         for i in range(args.warmup + args.steps):
             P.attend(i, c.stream, 1 / 16)
         c.torch.cuda.synchronize()
+        log("profile loop done")
+        return
+    if args.only == "cfg3_attn":
+        bench_cfg3(c, args.steps, args.warmup, n_layers=2, eager_only=True)
         log("profile loop done")
         return
 

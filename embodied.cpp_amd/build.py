@@ -26,8 +26,12 @@ ARCH = "gfx950"
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", f"-I{ROOT / 'include'}", f"-I{CSRC}", "-Wall",
           "-Wno-unused-function"]
+# -amdgpu-mfma-vgpr-form: MFMA accumulators stay in arch VGPRs.  Left to its
+# heuristic the compiler keeps the attention accumulators in AGPRs and, because
+# the (rarely taken) online-softmax rescale multiplies them with VALU ops,
+# copies all of them AGPR -> VGPR at the top of every key tile.
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-          "-munsafe-fp-atomics"]
+          "-munsafe-fp-atomics", "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
 
 def _compile(src: Path, asm: bool) -> Path:

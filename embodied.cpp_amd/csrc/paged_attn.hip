@@ -53,6 +53,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int WAVES = 4;
 constexpr int ROWS_PER_WAVE = 32;
@@ -138,40 +140,75 @@ struct Loader {
 
     // Keys of the tile are k0 + [0, KT).  Without a valid-slot list, key j is
     // logical slot j, so every 8-key group of V is contiguous inside one page
-    // and pages[] (the tile's KT/16 page ids, uniform over the workgroup) is
-    // all that is needed.
-    __device__ __forceinline__ void issue_direct(const KParams &p, const int32_t (&pages)[G::PAGES], int32_t k0,
-                                                 int32_t nk, int32_t kvh) {
+    // and the tile's KT/16 page ids (uniform over the workgroup) are all that
+    // is needed.  Each page is read through a buffer resource whose size
+    // covers only its valid rows (K) or nothing (an unmapped page), so the
+    // hardware range check returns zeros where the key list ends, without
+    // branches.  lim = min(n_keys, capacity).
+    __device__ __forceinline__ void issue_direct(const KParams &p, const int32_t *pt, int32_t k0, int32_t lim,
+                                                 int32_t kvh) {
         const int tid = threadIdx.x;
-        nk = min(nk, p.capacity);  // slots at or past the capacity are zero rows
+        int32_t pid[G::PAGES];
+        if constexpr (G::PAGES == 4) {
+            const i32x4 w = *reinterpret_cast<const i32x4 *>(pt);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pid[i] = w[i];
+        } else {
+            const i32x2 w = *reinterpret_cast<const i32x2 *>(pt);
+            pid[0] = w[0];
+            pid[1] = w[1];
+        }
+        __amdgpu_buffer_rsrc_t kr[G::PAGES], vr[G::PAGES];
+#pragma unroll
+        for (int pg = 0; pg < G::PAGES; ++pg) {
+            const int32_t page = __builtin_amdgcn_readfirstlane(pid[pg]);
+            const int32_t first = k0 + pg * 16;
+            const int32_t rows = page < 0 ? 0 : min(max(lim - first, 0), 16);
+            const int64_t pk = page < 0 ? 0 : ((int64_t)page * p.hkv + kvh) * (16 * D);
+            kr[pg] = __builtin_amdgcn_make_buffer_rsrc((void *)(p.k_pool + pk), 0, rows * D * 2, 0x00020000);
+            vr[pg] = __builtin_amdgcn_make_buffer_rsrc((void *)(p.v_pool + pk), 0, rows > 0 ? 16 * D * 2 : 0,
+                                                       0x00020000);
+        }
+        // Page of a chunk.  A page holds 16*CH K chunks and 2*D V chunks; at
+        // D >= 128 that is >= 256, so chunk i of every thread lies in page
+        // i*256/(page chunks), a constant.  At D = 64 a page is 128 chunks and
+        // the lower and upper 128 threads read consecutive pages (a choice
+        // between two descriptors on a wave-uniform condition).
+        const bool upper = __builtin_amdgcn_readfirstlane(tid >> 7) != 0;
 #pragma unroll
         for (int i = 0; i < G::KPT; ++i) {
             const int c = tid + i * 256;
             const int key = c / G::CH, dc = c % G::CH;
-            const int32_t j = k0 + key;
-            const int32_t page = pages[key >> 4];
-            k[i] = u32x4{0u, 0u, 0u, 0u};
-            if (j < nk && page >= 0)
-                k[i] = *reinterpret_cast<const u32x4 *>(p.k_pool + (((int64_t)page * p.hkv + kvh) * 16 + (j & 15)) * D +
-                                                        dc * 8);
+            __amdgpu_buffer_rsrc_t r;
+            if constexpr (16 * G::CH >= 256)
+                r = kr[i * 256 / (16 * G::CH)];
+            else
+                r = upper ? kr[2 * i + 1] : kr[2 * i];
+            k[i] = __builtin_bit_cast(u32x4,
+                                      __builtin_amdgcn_raw_buffer_load_b128(r, ((key & 15) * D + dc * 8) * 2, 0, 0));
         }
 #pragma unroll
         for (int i = 0; i < G::VPT; ++i) {
             const int c = tid + i * 256;
-            const int pg = c / (2 * D);
             const int rem = c % (2 * D);
             const int d = rem >> 1, half = rem & 1;
-            const int32_t jb = k0 + pg * 16 + half * 8;
-            const int32_t page = pages[pg];
-            v[i] = u32x4{0u, 0u, 0u, 0u};
-            if (jb < nk && page >= 0) {
-                v[i] = *reinterpret_cast<const u32x4 *>(p.v_pool + (((int64_t)page * p.hkv + kvh) * D + d) * 16 +
-                                                        half * 8);
-                if (jb + 8 > nk) {  // group straddles the key count: zero the tail keys
+            __amdgpu_buffer_rsrc_t r;
+            if constexpr (2 * D >= 256)
+                r = vr[i * 256 / (2 * D)];
+            else
+                r = upper ? vr[2 * i + 1] : vr[2 * i];
+            v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (d * 16 + half * 8) * 2, 0, 0));
+        }
+        if (k0 + G::KT > lim) {  // last tile: zero V of the keys past the end
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (jb + e >= nk) v[i][e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
-                }
+            for (int i = 0; i < G::VPT; ++i) {
+                const int c = tid + i * 256;
+                const int pg = c / (2 * D);
+                const int half = (c % (2 * D)) & 1;
+                const int32_t jb = k0 + pg * 16 + half * 8;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (jb + e >= lim) v[i][e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
             }
         }
     }
@@ -259,13 +296,13 @@ struct Loader {
     }
 };
 
-template <int D>
-__device__ __forceinline__ void load_pages(const int32_t *bt_b, int32_t k0, int32_t nk, int32_t capacity,
-                                           int32_t (&pages)[Geo<D>::PAGES]) {
-#pragma unroll
-    for (int pg = 0; pg < Geo<D>::PAGES; ++pg) {
-        const int32_t j = k0 + pg * 16;
-        pages[pg] = (j < nk && j < capacity) ? page_of(bt_b, j) : -1;
+constexpr int SEG_PAGES = 1024;  // block-table entries held in LDS at a time (16384 keys)
+
+// pt[i] = page id of page index seg_p0 + i, or -1 at and past p_end.
+__device__ __forceinline__ void load_segment(const int32_t *bt_b, int32_t seg_p0, int32_t p_end, int32_t *pt) {
+    for (int i = threadIdx.x; i < SEG_PAGES; i += 256) {
+        const int32_t pi = seg_p0 + i;
+        pt[i] = pi < p_end ? page_of(bt_b, pi * 16) : -1;
     }
 }
 
@@ -273,6 +310,7 @@ template <int D, int MASK, bool VALID, bool QF32>
 __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams p) {
     using G = Geo<D>;
     __shared__ __attribute__((aligned(16))) uint16_t smem[2 * G::STAGE];
+    __shared__ __attribute__((aligned(16))) int32_t pt[VALID ? 4 : SEG_PAGES];
 
     // XCD-aware order: hardware ids go round-robin over the 8 XCDs, so logical
     // work ids are handed out in contiguous runs per XCD, keeping the row tiles
@@ -329,6 +367,10 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                     w = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(p.q) + qoff + kk * 16);
                 }
             }
+            // At D = 256 the accumulators (128) and the rest of the loop fill the
+            // 256 arch VGPRs; the read-only query fragment lives in AGPRs, which
+            // MFMA reads directly.
+            if (D >= 256) asm volatile("" : "+a"(w));
             qf[kk] = __builtin_bit_cast(bf16x8, w);
         }
     }
@@ -362,19 +404,26 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     float m_run = -INFINITY, l_run = 0.0f;
 
     Loader<D, VALID> ld;
-    int32_t pages_n[G::PAGES], pages_nn[G::PAGES];  // tiles t+1 and t+2
+    const int32_t lim = min(nk, p.capacity);  // slots at or past the capacity are zero rows
+    const int32_t p_end = (min(lim, t_hi * G::KT) + 15) / 16;
+    int32_t seg_p0 = t_lo * G::PAGES;
     if (t_lo < t_hi) {
         if (VALID) {
             ld.issue_valid(p, valid_b, bt_b, t_lo * G::KT, nk, kvh);
         } else {
-            int32_t pg0[G::PAGES];
-            load_pages<D>(bt_b, t_lo * G::KT, nk, p.capacity, pg0);
-            ld.issue_direct(p, pg0, t_lo * G::KT, nk, kvh);
-            load_pages<D>(bt_b, (t_lo + 1) * G::KT, nk, p.capacity, pages_n);
+            load_segment(bt_b, seg_p0, p_end, pt);
+            __syncthreads();
+            ld.issue_direct(p, pt, t_lo * G::KT, lim, kvh);
         }
         ld.store(smem);
         __syncthreads();
     }
+    // Every load issued so far (the query fragment included) has landed.
+    // Without this the compiler, merging the path that skips the prologue,
+    // treats the query registers as possibly in flight inside the loop and
+    // waits for all outstanding loads -- the next tile's prefetch included --
+    // before the first MFMA of every tile.
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
 
     for (int32_t t = t_lo; t < t_hi; ++t) {
         const int32_t k0 = t * G::KT;
@@ -387,8 +436,14 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             if (VALID) {
                 ld.issue_valid(p, valid_b, bt_b, k0 + G::KT, nk, kvh);
             } else {
-                ld.issue_direct(p, pages_n, k0 + G::KT, nk, kvh);
-                load_pages<D>(bt_b, k0 + 2 * G::KT, nk, p.capacity, pages_nn);
+                int32_t pi = (t + 1) * G::PAGES - seg_p0;
+                if (pi + G::PAGES > SEG_PAGES) {  // next block-table segment (every wave is past its last read)
+                    seg_p0 = (t + 1) * G::PAGES;
+                    load_segment(bt_b, seg_p0, p_end, pt);
+                    __syncthreads();
+                    pi = 0;
+                }
+                ld.issue_direct(p, pt + pi, k0 + G::KT, lim, kvh);
             }
         }
 
@@ -410,13 +465,12 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
         bool tile_full = k0 + G::KT <= nk;
         if (MASK == EMB_MASK_CHUNK) tile_full = tile_full && k0 >= full_lo && k0 + G::KT <= full_hi;
         if (MASK == EMB_MASK_TOKEN || MASK == EMB_MASK_ADD || MASK == EMB_MASK_BLOCKMAP) tile_full = false;
-        float mt = -INFINITY;
+        if (!tile_full) {  // one uniform branch around the whole per-key mask
 #pragma unroll
-        for (int kb = 0; kb < G::KB; ++kb) {
+            for (int kb = 0; kb < G::KB; ++kb) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float x = s[kb][r];
-                if (!tile_full) {
+                for (int r = 0; r < 16; ++r) {
+                    float x = s[kb][r];
                     const int32_t j = k0 + kb * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
                     bool vis = row_ok && j < nk;
                     if (MASK == EMB_MASK_CHUNK) {
@@ -436,12 +490,15 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                             vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
                                                                             (int64_t)tok * p.mask_q_stride + j] != 0;
                     }
-                    if (!vis) x = -INFINITY;
-                    s[kb][r] = x;
+                    s[kb][r] = vis ? x : -INFINITY;
                 }
-                mt = fmaxf(mt, x);
             }
         }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         // (4) wave-uniform lazy rescale
         if (__builtin_amdgcn_ballot_w64(mt > m_run + p.th_raw) != 0) {
@@ -477,13 +534,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                 }
 
         // (6) hand tile t+1 over through the other LDS stage
-        if (more) {
-            ld.store(nxt);
-            if (!VALID) {
-#pragma unroll
-                for (int i = 0; i < G::PAGES; ++i) pages_n[i] = pages_nn[i];
-            }
-        }
+        if (more) ld.store(nxt);
         __syncthreads();
     }
 
