@@ -350,6 +350,69 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
                 flops_per_layer=fl_layer, layers=n_layers)
 
 
+def _bf16_bits(f: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(f, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bench_cfg5(c: Ctx, steps, warmup):
+    """W8A16 QKV projection (1560 x 3072 -> 3 x 3072, int8 Marlin layout, bf16 scales) alone, and
+    fused with the append of its K/V slices into a config-3 paged cache followed by the config-3
+    attention over 14040 keys (one layer)."""
+    torch, emb = c.torch, c.emb
+    M, K, H, d, C, W = 1560, 3072, 24, 128, 1560, 9
+    N = 3 * H * d
+    x = c.synth(0xE3BD0004 + 1, M * K)
+    g = np.random.default_rng(0xE3BD0004)
+    # u8 = w + 128 with w ~ U[-127, 127]: uniform random bytes in [1, 255] are a uniform random
+    # weight in any byte order, so the Marlin payload is drawn directly
+    qw = torch.from_numpy(g.integers(1, 256, (K // 16, 16 * N), dtype=np.uint8).view(np.int32)).to(c.dev)
+    sc = torch.from_numpy(_bf16_bits(g.uniform(0.001, 0.01, N).astype(np.float32)).view(np.int16)).to(c.dev)
+    y = torch.empty((M, N), dtype=torch.int16, device=c.dev)
+    flops = 2.0 * M * K * N
+
+    def gemm(st):
+        emb.w8a16_gemm(x, qw, sc, M, K, N, y, stream=st)
+    ms_g, _ = c.time_graph(gemm, steps, warmup)
+    k_launch = 10
+
+    def gemm_many(st):
+        for _ in range(k_launch):
+            emb.w8a16_gemm(x, qw, sc, M, K, N, y, stream=st)
+    ms_many, _ = c.time_graph(gemm_many, max(2, steps // 4), 2)
+    gemm_us = ms_many * 1e3 / k_launch
+
+    cap = C * W
+    pages = (cap + 15) // 16
+    bt = c.i32(g.permutation(pages))
+    page_elems = H * 16 * d
+    kp = torch.zeros(pages * page_elems, dtype=torch.int16, device=c.dev)
+    vp = torch.zeros_like(kp)
+    kv0 = c.synth(0xE3BD0004 + 2, cap * H * d)
+    emb.kv_append(kv0, kv0, H * d, cap, c.i32(np.arange(cap)), bt, cap, kp, vp, H, d)
+    qo = torch.empty((M, H * d), dtype=torch.int16, device=c.dev)
+    slots = c.i32(np.arange(C))  # the new chunk takes the slots of the evicted oldest chunk
+    out = torch.empty((C, H, d), dtype=torch.float32, device=c.dev)
+    cu, nk = c.i32([0, C]), c.i32([cap])
+
+    def fused(st):
+        emb.w8a16_qkv_append(x, qw, sc, M, K, H * d, qo, slots, bt, cap, kp, vp, H, d, stream=st)
+
+    def step(st):
+        fused(st)
+        emb.paged_attention(q=qo, out=out, k_pool=kp, v_pool=vp, batch=1, hq=H, hkv=H, d=d, max_q=C,
+                            scale=1 / math.sqrt(d), capacity=cap, cu_q=cu, n_keys=nk, block_tables=bt,
+                            bt_stride=pages, stream=st)
+    ms_f, _ = c.time_graph(fused, steps, warmup)
+    ms_s, _ = c.time_graph(step, max(2, steps // 4), 2)
+    gemm_bytes = M * K * 2 + K * N + N * 2 + M * N * 2
+    return dict(gemm_us=gemm_us, gemm_us_single_launch=ms_g * 1e3, gemm_tflops=flops / (gemm_us * 1e-6) / 1e12,
+                gemm_mfma_frac=flops / (gemm_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, gemm_flops=flops,
+                gemm_bytes=gemm_bytes, fused_qkv_append_us=ms_f * 1e3,
+                fused_plus_attention_us_per_layer=ms_s * 1e3)
+
+
 class MT64:
     """std::mt19937_64 (for drawing config-4 prefix lengths)."""
 
@@ -437,7 +500,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="cfg1,cfg2,cfg3,cfg4")
+    ap.add_argument("--configs", default="cfg1,cfg2,cfg3,cfg4,cfg5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="cfg1_attn: only the headline kernel loop (profiling)")
     args = ap.parse_args()
@@ -454,6 +517,10 @@ def main():
         for i in range(args.warmup + args.steps):
             P.attend(i, c.stream, 1 / 16)
         c.torch.cuda.synchronize()
+        log("profile loop done")
+        return
+    if args.only == "cfg5_gemm":
+        bench_cfg5(c, args.steps, args.warmup)
         log("profile loop done")
         return
     if args.only == "cfg3_attn":
@@ -479,6 +546,10 @@ def main():
         log("cfg3 ...")
         extra["cfg3"] = bench_cfg3(c, args.steps, args.warmup)
         log("cfg3", json.dumps(extra["cfg3"]))
+    if "cfg5" in cfgs:
+        log("cfg5 ...")
+        extra["cfg5"] = bench_cfg5(c, args.steps, args.warmup)
+        log("cfg5", json.dumps(extra["cfg5"]))
 
     cpu = None
     if not args.no_cpu:

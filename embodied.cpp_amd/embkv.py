@@ -97,7 +97,18 @@ _SIGS = {
     "lingbot_runtime_kv_attn_cublas_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int,
                                                      C.c_int, C.c_int, C.c_int, C.c_float, vp]),
     "emb_synth_normal_bf16": (C.c_int, [C.c_uint64, C.c_int64, u16p]),
+    "emb_w8a16_gemm": (C.c_int, [vp, C.c_int32, C.c_int64, vp, vp, C.c_int32, C.c_int32, C.c_int32,
+                                 vp, C.c_int64, C.c_int32, vp]),
+    "emb_w8a16_qkv_append": (C.c_int, [vp, C.c_int32, C.c_int64, vp, vp, C.c_int32, C.c_int32,
+                                       C.c_int32, vp, C.c_int64, vp, vp, C.c_int32, vp, vp,
+                                       C.c_int32, C.c_int32, vp]),
+    "cosmos3_w8a16_linear_f32": (C.c_int, [vp, vp, vp, vp] + [C.c_int] * 7 + [vp]),
+    "cosmos3_w8a16_linear_f32_ws": (C.c_int, [vp] * 8 + [C.c_int] * 7 + [vp]),
+    "cosmos3_w8a16_linear_bf16_ws": (C.c_int, [vp] * 7 + [C.c_int] * 7 + [vp]),
+    "cosmos3_w8a16_f32_to_bf16_ws": (C.c_int, [vp, vp, C.c_int, vp]),
 }
+
+EMB_W8_Y_BF16, EMB_W8_Y_F32_ROUNDED, EMB_W8_Y_F32_RAW = range(3)
 
 
 def header_symbols() -> list[str]:
@@ -272,6 +283,22 @@ def kv_gather(k_pool, v_pool, valid, n, block_table, capacity, k_out, v_out, hkv
     return check(lib().emb_kv_gather(ptr(k_pool), ptr(v_pool), ptr(valid), n, ptr(block_table),
                                      capacity, ptr(k_out), ptr(v_out), hkv, d, stream_ptr(stream)),
                  "emb_kv_gather")
+
+
+def w8a16_gemm(x, qweight, scales, M, K, N, y, y_kind=EMB_W8_Y_BF16, x_is_f32=False, ldx=None,
+               ldy=None, stream=None):
+    return check(lib().emb_w8a16_gemm(ptr(x), int(x_is_f32), ldx or K, ptr(qweight), ptr(scales),
+                                       M, K, N, ptr(y), ldy or N, y_kind, stream_ptr(stream)),
+                 "emb_w8a16_gemm")
+
+
+def w8a16_qkv_append(x, qweight, scales, M, K, n_q, q_out, slots, block_table, capacity, k_pool,
+                     v_pool, hkv, d, x_is_f32=False, ldx=None, ldq=None, stream=None):
+    return check(lib().emb_w8a16_qkv_append(ptr(x), int(x_is_f32), ldx or K, ptr(qweight),
+                                            ptr(scales), M, K, n_q, ptr(q_out), ldq or n_q,
+                                            ptr(slots), ptr(block_table), capacity, ptr(k_pool),
+                                            ptr(v_pool), hkv, d, stream_ptr(stream)),
+                 "emb_w8a16_qkv_append")
 
 
 def attn_workspace_bytes(batch, max_q, hq, hkv, d, splits):

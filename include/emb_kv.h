@@ -226,6 +226,64 @@ int lingbot_runtime_kv_attn_cublas_f32(const float *q, const float *cache_k,
                                        int seq_q, int seq_k, int n_heads, int head_dim,
                                        int capacity, float scale, hipStream_t stream);
 
+/* ============================================================
+ * W8A16 linear (int8 weight-only, Marlin kU8B128 channelwise layout)
+ * y[m][n] = bf16( (sum_k bf16(x[m][k]) * (u8[k][n] - 128)) * s[n] ), fp32
+ * accumulate, the scale applied to the fp32 accumulator -- the numerics of
+ * cosmos3_w8a16_linear_* over vllm Marlin
+ * (kernels/cosmos3/cosmos3_w8_marlin_cuda.cu:302-501,651-765).
+ * qweight: int32 [K/16][4N] in the layout of marlin_w8_dst_byte
+ * (cosmos3_w8_marlin_cuda.cu:50-58, kernels/cosmos3/README.md:55-64);
+ * scales: bf16 [N] in the order of marlin_scale_index (:79-88).
+ * Needs K % 16 == 0 and N % 64 == 0 (else EMB_ERR_UNSUPPORTED).
+ * ============================================================ */
+enum {
+    EMB_W8_Y_BF16 = 0,        /* y: bf16 [M][ldy] */
+    EMB_W8_Y_F32_ROUNDED = 1, /* y: f32 [M][ldy] holding the bf16-rounded value
+                                 (the reference's bf16 -> f32 widening, :407) */
+    EMB_W8_Y_F32_RAW = 2      /* y: f32 [M][ldy], the fp32 epilogue value before
+                                 the bf16 round (for numerics checks) */
+};
+/* x: bf16 (x_is_f32 == 0) or f32 (rounded to bf16 on load) [M][ldx]. */
+int emb_w8a16_gemm(const void *x, int32_t x_is_f32, int64_t ldx, const int32_t *qweight,
+                   const uint16_t *scales, int32_t M, int32_t K, int32_t N, void *y, int64_t ldy,
+                   int32_t y_kind, hipStream_t stream);
+
+/* The QKV projection that feeds the cache, with the append fused into its
+ * epilogue (no reference counterpart as one call: models/cosmos3.cpp:4941-4943
+ * makes three W8 calls and lingbot_runtime_kv_update_f32 then scatters K/V).
+ * Output columns: [0, n_q) -> q_out bf16 [M][ldq]; the next
+ * n_kv_heads*head_dim -> K and the last n_kv_heads*head_dim -> V, written as
+ * bf16 into the pool pages of logical slot slots[m] (same skip rules as
+ * emb_kv_append).  N = n_q + 2*n_kv_heads*head_dim. */
+int emb_w8a16_qkv_append(const void *x, int32_t x_is_f32, int64_t ldx, const int32_t *qweight,
+                         const uint16_t *scales, int32_t M, int32_t K, int32_t n_q, void *q_out,
+                         int64_t ldq, const int32_t *slots, const int32_t *block_table,
+                         int32_t capacity, void *k_pool, void *v_pool, int32_t n_kv_heads,
+                         int32_t head_dim, hipStream_t stream);
+
+/* Reference-named W8 face (kernels/cosmos3/cosmos3_w8_marlin_cuda.h:24-84 with
+ * hipStream_t).  y is f32 holding the bf16-rounded result.  The workspaces of
+ * the _ws variants are accepted and not used. */
+int cosmos3_w8a16_linear_f32(const float *x, const int *qweight, const unsigned short *scales_bf16,
+                             float *y, int batch, int in_features, int out_features,
+                             int qweight_rows, int qweight_cols, int scale_rows, int scale_cols,
+                             hipStream_t stream);
+int cosmos3_w8a16_linear_f32_ws(const float *x, const int *qweight,
+                                const unsigned short *scales_bf16, float *y,
+                                unsigned short *x_bf16_workspace, unsigned short *y_bf16_workspace,
+                                float *c_tmp_workspace, int *int_workspace, int batch,
+                                int in_features, int out_features, int qweight_rows,
+                                int qweight_cols, int scale_rows, int scale_cols, hipStream_t stream);
+int cosmos3_w8a16_linear_bf16_ws(const unsigned short *x_bf16, const int *qweight,
+                                 const unsigned short *scales_bf16, float *y,
+                                 unsigned short *y_bf16_workspace, float *c_tmp_workspace,
+                                 int *int_workspace, int batch, int in_features, int out_features,
+                                 int qweight_rows, int qweight_cols, int scale_rows, int scale_cols,
+                                 hipStream_t stream);
+int cosmos3_w8a16_f32_to_bf16_ws(const float *x, unsigned short *x_bf16_workspace, int count,
+                                 hipStream_t stream);
+
 /* Synthetic inputs for the bench: N(0,1) bf16 from std::mt19937_64(seed)
  * (Box-Muller on 53-bit uniforms), written to host memory. */
 int emb_synth_normal_bf16(uint64_t seed, int64_t n, uint16_t *out);

@@ -1,0 +1,227 @@
+"""GPU parity of the W8A16 (Marlin kU8B128 channelwise) linear and of its
+fused QKV -> paged-cache append, against the oracle.
+
+Bars:
+  * fp32 epilogue value (EMB_W8_Y_F32_RAW) within max-abs 2e-2 and mean-rel
+    1e-3 of the oracle; bit-exact where every
+    product and partial sum is an exactly representable integer, which pins
+    the Marlin byte layout, the k permutation and the scale permutation.
+  * bf16 outputs: the oracle rounds its own fp32 value, so a result that lies
+    within fp32 accumulation-order error of a rounding boundary may land one
+    bf16 ulp away (and a near-zero result, where the sum cancels, a few ulps of
+    its own tiny magnitude); the test requires |diff| <= 1 ulp + the fp32
+    accumulation bound everywhere and >= 99% of the elements bit-identical.
+    (The north-star max-abs 2e-2 cannot apply to bf16 outputs of magnitude
+    ~20, where one bf16 ulp is 0.125; it is applied to the fp32 value.)
+  * fused append: the Q buffer and the K/V pool rows are bit-identical to the
+    plain GEMM's bf16 output for the same columns (one kernel's numerics),
+    rows with a skipped slot leave the pool untouched.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return torch, torch.device("cuda")
+
+
+def _t(torch, dev, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to(dev)
+
+
+def _weights(orc, rng, K, N, s_lo=0.001, s_hi=0.01):
+    w = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    s = orc.f32_to_bf16(rng.uniform(s_lo, s_hi, N).astype(np.float32))
+    return w, orc.marlin_pack_w8(w), s, orc.marlin_pack_scales(s)
+
+
+def _gemm(emb, torch, dev, x, q, s_st, M, K, N, y_kind, x_is_f32=False):
+    if y_kind == emb.EMB_W8_Y_BF16:
+        y = torch.zeros((M, N), dtype=torch.int16, device=dev)
+    else:
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    emb.w8a16_gemm(_t(torch, dev, x), _t(torch, dev, q), _t(torch, dev, s_st), M, K, N, y, y_kind=y_kind,
+                   x_is_f32=x_is_f32)
+    torch.cuda.synchronize()
+    o = y.cpu().numpy()
+    return o.view(np.uint16) if y_kind == emb.EMB_W8_Y_BF16 else o
+
+
+def _check_bf16(got, ref, what, orc):
+    """|got - ref| <= one bf16 ulp of ref + the fp32 accumulation-order bound
+    (2^-17 of the largest |ref|: K <= 3072 products summed in fp32, measured
+    below 1e-6 relative in test_w8_random_against_oracle), and >= 99% of the
+    elements bit-identical."""
+    g = orc.bf16_to_f32(got).astype(np.float64)
+    r = orc.bf16_to_f32(ref).astype(np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(r), 1e-30))) - 7)
+    bound = ulp + 2.0 ** -17 * np.abs(r).max()
+    bad = np.abs(g - r) > bound
+    assert not bad.any(), f"{what}: {bad.sum()} elements beyond 1 ulp + fp32 bound"
+    same = (got == ref).mean()
+    assert same >= 0.99, f"{what}: only {same:.4f} bit-identical"
+
+
+@pytest.mark.parametrize("M,K,N", [(40, 96, 192), (7, 16, 64), (257, 192, 320)])
+def test_w8_exact_integer_layout(emb, orc, torch_dev, M, K, N):
+    """Small integer x and unit scales: every partial sum is exact in fp32, so
+    the GPU must reproduce the oracle bit for bit.  Shapes cover a partial
+    k-tile (K % 64 != 0), a partial n-tile (N % 128 == 64) and partial m-tiles."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(M * 1000 + K + N)
+    w = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    q = orc.marlin_pack_w8(w)
+    s = np.full(N, 0x3F80, np.uint16)  # bf16 1.0
+    s_st = orc.marlin_pack_scales(s)
+    x = orc.f32_to_bf16(rng.integers(-3, 4, (M, K)).astype(np.float32))
+    yb_ref, yf_ref = orc.w8a16_gemm(x, q, s_st, M, K, N)
+    exact = orc.bf16_to_f32(x).astype(np.float64) @ w.astype(np.float64)
+    assert np.array_equal(yf_ref, exact.astype(np.float32))  # the oracle itself is exact here
+    yf = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_F32_RAW)
+    assert np.array_equal(yf, yf_ref), "W8 fp32 result differs from the exact integer product"
+    yb = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_BF16)
+    assert np.array_equal(yb, yb_ref)
+    yr = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_F32_ROUNDED)
+    assert np.array_equal(yr, orc.bf16_to_f32(yb_ref))
+
+
+def test_w8_scale_permutation_exact(emb, orc, torch_dev):
+    """Power-of-two per-channel scales keep the result exact and make a wrong
+    scale permutation visible column by column."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(11)
+    M, K, N = 33, 64, 256
+    w = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    q = orc.marlin_pack_w8(w)
+    s = orc.f32_to_bf16((2.0 ** rng.integers(-12, -2, N)).astype(np.float32))
+    s_st = orc.marlin_pack_scales(s)
+    x = orc.f32_to_bf16(rng.integers(-4, 5, (M, K)).astype(np.float32))
+    _, yf_ref = orc.w8a16_gemm(x, q, s_st, M, K, N)
+    yf = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_F32_RAW)
+    assert np.array_equal(yf, yf_ref)
+
+
+def test_w8_random_against_oracle(emb, orc, torch_dev):
+    torch, dev = torch_dev
+    rng = np.random.default_rng(5)
+    M, K, N = 300, 512, 384
+    w, q, s, s_st = _weights(orc, rng, K, N)
+    x = orc.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    yb_ref, yf_ref = orc.w8a16_gemm(x, q, s_st, M, K, N)
+    yf = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_F32_RAW)
+    mx, mr = assert_close(yf, yf_ref, "w8 fp32")
+    assert mr < 1e-5, f"fp32 accumulation error unexpectedly large: {mr:.2e}"
+    yb = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_BF16)
+    _check_bf16(yb, yb_ref, "w8 bf16", orc)
+
+
+def test_w8_reference_named_faces(emb, orc, torch_dev):
+    """cosmos3_w8a16_linear_{f32,f32_ws,bf16_ws}: f32 input rounded to bf16,
+    y = f32 of the bf16 result; shape checks return -1 like the reference."""
+    torch, dev = torch_dev
+    L = emb.lib()
+    rng = np.random.default_rng(9)
+    M, K, N = 45, 256, 192
+    w, q, s, s_st = _weights(orc, rng, K, N)
+    xf = rng.standard_normal((M, K)).astype(np.float32)
+    xb = orc.f32_to_bf16(xf)
+    yb_ref, _ = orc.w8a16_gemm(xb, q, s_st, M, K, N)
+    xf_d, xb_d = _t(torch, dev, xf), _t(torch, dev, xb)
+    q_d, s_d = _t(torch, dev, q), _t(torch, dev, s_st.reshape(1, N))
+    outs = []
+    for face in ("f32", "f32_ws", "bf16_ws"):
+        y = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+        if face == "f32":
+            rc = L.cosmos3_w8a16_linear_f32(xf_d.data_ptr(), q_d.data_ptr(), s_d.data_ptr(), y.data_ptr(), M, K, N,
+                                            K // 16, N * 4, 1, N, None)
+        elif face == "f32_ws":
+            ws = torch.empty(M * K, dtype=torch.int16, device=dev)
+            rc = L.cosmos3_w8a16_linear_f32_ws(xf_d.data_ptr(), q_d.data_ptr(), s_d.data_ptr(), y.data_ptr(),
+                                               ws.data_ptr(), None, None, None, M, K, N, K // 16, N * 4, N, 1, None)
+        else:
+            rc = L.cosmos3_w8a16_linear_bf16_ws(xb_d.data_ptr(), q_d.data_ptr(), s_d.data_ptr(), y.data_ptr(), None,
+                                                None, None, M, K, N, K // 16, N * 4, 1, N, None)
+        assert rc == 0, emb.last_error()
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    for o in outs:
+        _check_bf16(orc.f32_to_bf16(o), yb_ref, "cosmos3 face", orc)
+        assert np.array_equal(o, outs[0])
+    # the f32_to_bf16 helper rounds to nearest even
+    xw = torch.zeros(M * K, dtype=torch.int16, device=dev)
+    assert L.cosmos3_w8a16_f32_to_bf16_ws(xf_d.data_ptr(), xw.data_ptr(), M * K, None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(xw.cpu().numpy().view(np.uint16), xb.reshape(-1))
+    # bad shapes are rejected before any launch
+    y = torch.zeros((M, N), dtype=torch.float32, device=dev)
+    assert L.cosmos3_w8a16_linear_f32(xf_d.data_ptr(), q_d.data_ptr(), s_d.data_ptr(), y.data_ptr(), M, K, N,
+                                      K // 16 + 1, N * 4, 1, N, None) == -1
+    assert L.cosmos3_w8a16_linear_f32(xf_d.data_ptr(), q_d.data_ptr(), s_d.data_ptr(), y.data_ptr(), M, K, N,
+                                      K // 16, N * 4, 2, N, None) == -1
+
+
+def test_w8_qkv_append_matches_gemm(emb, orc, torch_dev):
+    """The fused projection writes exactly the plain GEMM's bf16 values: Q into
+    its buffer, K/V into the pool rows of slots[m] through a permuted block
+    table; skipped slots (-1, >= capacity, unmapped page) leave the pool as is."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(21)
+    M, K, n_q, hkv, d = 70, 128, 256, 2, 64
+    n_kv = hkv * d
+    N = n_q + 2 * n_kv
+    w, q, s, s_st = _weights(orc, rng, K, N)
+    x = orc.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    cap = 128
+    n_pages = cap // 16
+    bt = rng.permutation(n_pages + 3)[:n_pages].astype(np.int32)
+    bt[5] = -1  # one unmapped page
+    slots = rng.permutation(cap)[:M].astype(np.int32)
+    slots[3], slots[10] = -1, cap + 7
+    page_elems = hkv * 16 * d
+    kp0 = rng.integers(0, 0x3F00, (n_pages + 3) * page_elems, dtype=np.uint16)
+    vp0 = rng.integers(0, 0x3F00, (n_pages + 3) * page_elems, dtype=np.uint16)
+    x_d, q_d, s_d = _t(torch, dev, x), _t(torch, dev, q), _t(torch, dev, s_st)
+    kp, vp = _t(torch, dev, kp0), _t(torch, dev, vp0)
+    qo = torch.zeros((M, n_q), dtype=torch.int16, device=dev)
+    emb.w8a16_qkv_append(x_d, q_d, s_d, M, K, n_q, qo, _t(torch, dev, slots), _t(torch, dev, bt), cap, kp, vp,
+                         hkv, d)
+    torch.cuda.synchronize()
+    yb = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_BF16)
+    assert np.array_equal(qo.cpu().numpy().view(np.uint16), yb[:, :n_q])
+    # expected pool: the oracle's paged append of the plain GEMM's K/V columns
+    kexp, vexp = kp0.copy(), vp0.copy()
+    kcols = np.ascontiguousarray(yb[:, n_q:n_q + n_kv])
+    vcols = np.ascontiguousarray(yb[:, n_q + n_kv:])
+    orc.paged_append(kcols, vcols, n_kv, slots, bt, hkv, d, cap, kexp, vexp)
+    assert np.array_equal(kp.cpu().numpy().view(np.uint16), kexp), "K pages differ"
+    assert np.array_equal(vp.cpu().numpy().view(np.uint16), vexp), "V pages differ"
+    # and the bf16 GEMM itself is within the bf16 bar of the oracle
+    yb_ref, _ = orc.w8a16_gemm(x, q, s_st, M, K, N)
+    _check_bf16(yb, yb_ref, "qkv gemm", orc)
+
+
+def test_w8_config5_shape_sampled_rows(emb, orc, torch_dev):
+    """BASELINE configs[4] shape (1560 x 3072 -> 9216) on the GPU; the oracle
+    checks 24 rows spread over the m-tiles (first, last and the tile edges)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0004)
+    M, K, N = 1560, 3072, 9216
+    w, q, s, s_st = _weights(orc, rng, K, N)
+    x = orc.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    yf = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_F32_RAW)
+    rows = np.array(sorted({0, 1, 255, 256, 511, 512, 767, 1023, 1024, 1279, 1280, 1535, 1536, 1550, 1558, 1559,
+                            *rng.integers(0, M, 8).tolist()}), np.int64)
+    _, yf_ref = orc.w8a16_gemm(x, q, s_st, M, K, N, rows=rows)
+    assert_close(yf[rows], yf_ref, "w8 config-5 rows")
