@@ -117,6 +117,7 @@ class PagedLayers:
         page_elems = hkv * 16 * d
         self.k_pool = torch.zeros(total_pages * page_elems, dtype=torch.int16, device=c.dev)
         self.v_pool = torch.zeros_like(self.k_pool)
+        self.v16_pool = torch.zeros_like(self.k_pool)  # f16 V shadow (zero-filled)
         # prefix K/V appended through the library (one combined slot space:
         # cache b's slot s is logical slot b*cap + s of one concatenated table)
         tot_pref = sum(self.n_prefix)
@@ -125,7 +126,7 @@ class PagedLayers:
             vpre = c.synth(seed + 2, tot_pref * hkv * d)
             slots = np.concatenate([b * self.cap + np.arange(p) for b, p in enumerate(self.n_prefix)])
             emb.kv_append(kpre, vpre, hkv * d, tot_pref, c.i32(slots), self.bt, self.L * self.cap,
-                          self.k_pool, self.v_pool, hkv, d)
+                          self.k_pool, self.v_pool, hkv, d, v16_pool=self.v16_pool)
         # per-step new K/V and Q
         self.new_slots = c.i32(np.concatenate([b * self.cap + p + np.arange(n_new)
                                                for b, p in enumerate(self.n_prefix)]))
@@ -149,11 +150,12 @@ class PagedLayers:
         s = step % self.n_steps
         self.c.emb.kv_append(self.knew[s], self.vnew[s], self.hkv * self.d, self.L * self.n_new,
                              self.new_slots, self.bt, self.L * self.cap, self.k_pool, self.v_pool,
-                             self.hkv, self.d, stream=stream)
+                             self.hkv, self.d, stream=stream, v16_pool=self.v16_pool)
 
     def attend(self, step, stream, scale):
         s = step % self.n_steps
         self.c.emb.paged_attention(q=self.q[s], out=self.out, k_pool=self.k_pool, v_pool=self.v_pool,
+                                   v16_pool=self.v16_pool,
                                    batch=self.L, hq=self.hq, hkv=self.hkv, d=self.d, max_q=self.n_new,
                                    scale=scale, capacity=self.cap, cu_q=self.cu_q, n_keys=self.nk,
                                    block_tables=self.bt, bt_stride=self.bt_stride, splits=self.splits,
@@ -315,9 +317,10 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
         bt = g.permutation(pages).astype(np.int32)
         kp = torch.empty(pages * page_elems, dtype=torch.int16, device=c.dev)
         vp = torch.empty_like(kp)
+        v16 = torch.zeros_like(kp)
         bt_d = c.i32(bt)
-        emb.kv_append(base_k, base_v, H * d, cap, c.i32(np.arange(cap)), bt_d, cap, kp, vp, H, d)
-        pools.append((kp, vp, bt_d))
+        emb.kv_append(base_k, base_v, H * d, cap, c.i32(np.arange(cap)), bt_d, cap, kp, vp, H, d, v16_pool=v16)
+        pools.append((kp, vp, v16, bt_d))
     out = torch.empty((C, H, d), dtype=torch.float32, device=c.dev)
     cu = c.i32([0, C])
     nk = c.i32([cap])
@@ -326,10 +329,10 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
     scale = 1 / math.sqrt(d)
 
     def layer(l, st, append=True):
-        kp, vp, bt = pools[l]
+        kp, vp, v16, bt = pools[l]
         if append:
-            emb.kv_append(knew, vnew, H * d, C, new_slots, bt, cap, kp, vp, H, d, stream=st)
-        emb.paged_attention(q=q, out=out, k_pool=kp, v_pool=vp, batch=1, hq=H, hkv=H, d=d, max_q=C,
+            emb.kv_append(knew, vnew, H * d, C, new_slots, bt, cap, kp, vp, H, d, stream=st, v16_pool=v16)
+        emb.paged_attention(q=q, out=out, k_pool=kp, v_pool=vp, v16_pool=v16, batch=1, hq=H, hkv=H, d=d, max_q=C,
                             scale=scale, capacity=cap, cu_q=cu, n_keys=nk, block_tables=bt, bt_stride=pages,
                             stream=st)
 
@@ -389,19 +392,20 @@ def bench_cfg5(c: Ctx, steps, warmup):
     page_elems = H * 16 * d
     kp = torch.zeros(pages * page_elems, dtype=torch.int16, device=c.dev)
     vp = torch.zeros_like(kp)
+    v16 = torch.zeros_like(kp)
     kv0 = c.synth(0xE3BD0004 + 2, cap * H * d)
-    emb.kv_append(kv0, kv0, H * d, cap, c.i32(np.arange(cap)), bt, cap, kp, vp, H, d)
+    emb.kv_append(kv0, kv0, H * d, cap, c.i32(np.arange(cap)), bt, cap, kp, vp, H, d, v16_pool=v16)
     qo = torch.empty((M, H * d), dtype=torch.int16, device=c.dev)
     slots = c.i32(np.arange(C))  # the new chunk takes the slots of the evicted oldest chunk
     out = torch.empty((C, H, d), dtype=torch.float32, device=c.dev)
     cu, nk = c.i32([0, C]), c.i32([cap])
 
     def fused(st):
-        emb.w8a16_qkv_append(x, qw, sc, M, K, H * d, qo, slots, bt, cap, kp, vp, H, d, stream=st)
+        emb.w8a16_qkv_append(x, qw, sc, M, K, H * d, qo, slots, bt, cap, kp, vp, H, d, stream=st, v16_pool=v16)
 
     def step(st):
         fused(st)
-        emb.paged_attention(q=qo, out=out, k_pool=kp, v_pool=vp, batch=1, hq=H, hkv=H, d=d, max_q=C,
+        emb.paged_attention(q=qo, out=out, k_pool=kp, v_pool=vp, v16_pool=v16, batch=1, hq=H, hkv=H, d=d, max_q=C,
                             scale=1 / math.sqrt(d), capacity=cap, cu_q=cu, n_keys=nk, block_tables=bt,
                             bt_stride=pages, stream=st)
     ms_f, _ = c.time_graph(fused, steps, warmup)

@@ -21,6 +21,17 @@ inline uint16_t f32_to_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+#if defined(__HIP__)  // device helpers, for the .hip sources
+// Element offset, inside one f16 V-shadow page of one kv head, of dim d and
+// page row t: the 16 keys of a dim sit in the order the attention P.V MFMA
+// reads them (row t at position P = t with bits 2 and 3 swapped), the two
+// 8-key halves exchanged when bit 3 of d is set (LDS bank spread).
+__host__ __device__ inline int v16_index(int d, int t) {
+    const int P = (t & 3) | ((t >> 1) & 4) | ((t << 1) & 8);
+    return d * 16 + (((P >> 3) ^ ((d >> 3) & 1)) << 3) + (P & 7);
+}
+#endif
+
 // std::mt19937_64-compatible engine (same constants as the C++ standard).
 struct Mt64 {
     uint64_t mt[312];

@@ -71,34 +71,44 @@ __device__ __forceinline__ u32x4 pack8(const uint16_t (&o)[8]) {
     return w;
 }
 
-// One thread per (token s, head h, 8-wide chunk c), s fastest.
+// One thread per (token s, head h, 8-wide chunk c), s fastest, so the 16
+// tokens of one page write one 32-byte V row together.  Index arithmetic is
+// 32-bit (the host checks that n*H*D/8 fits); only addresses are 64-bit.
+// With a V shadow, each element is also written as f16 at its position in the
+// attention MFMA's key order (emb::v16_index).
 template <typename Src>
 __global__ __launch_bounds__(256) void kv_append_kernel(const Src *__restrict__ k, const Src *__restrict__ v,
                                                         const int32_t *__restrict__ slots,
                                                         const int32_t *__restrict__ block_table,
                                                         uint16_t *__restrict__ k_pool,
-                                                        uint16_t *__restrict__ v_pool, MoveGeom g) {
-    const int64_t total = (int64_t)g.n * g.heads * g.chunks;
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (int64_t)gridDim.x * blockDim.x) {
-        const int32_t s = (int32_t)(idx % g.n);
-        const int64_t hc = idx / g.n;
-        const int32_t c = (int32_t)(hc % g.chunks);
-        const int32_t h = (int32_t)(hc / g.chunks);
+                                                        uint16_t *__restrict__ v_pool,
+                                                        uint16_t *__restrict__ v16_pool, MoveGeom g) {
+    const int32_t total = g.n * g.heads * g.chunks;
+    for (int32_t idx = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x); idx < total;
+         idx += (int32_t)(gridDim.x * blockDim.x)) {
+        const int32_t s = idx % g.n;
+        const int32_t hc = idx / g.n;
+        const int32_t c = hc % g.chunks;
+        const int32_t h = hc / g.chunks;
         const int32_t slot = slots[s];
         if (slot < 0 || slot >= g.capacity) continue;
         const int32_t page = block_table ? block_table[slot >> 4] : (slot >> 4);
         if (page < 0) continue;
         const int32_t t = slot & 15;
-        const int64_t src = (int64_t)s * g.src_stride + (int64_t)h * g.head_dim + c * 8;
+        const int64_t src = (int64_t)s * g.src_stride + h * g.head_dim + c * 8;
         uint16_t kv[8], vv[8];
         load8<Src>(k + src, kv);
         load8<Src>(v + src, vv);
-        const int64_t kdst = (((int64_t)page * g.heads + h) * 16 + t) * g.head_dim + c * 8;
-        *reinterpret_cast<u32x4 *>(k_pool + kdst) = pack8(kv);
-        const int64_t vdst = (((int64_t)page * g.heads + h) * g.head_dim + c * 8) * 16 + t;
+        const int64_t pbase = ((int64_t)page * g.heads + h) * 16 * g.head_dim;  // page element base
+        *reinterpret_cast<u32x4 *>(k_pool + pbase + t * g.head_dim + c * 8) = pack8(kv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v_pool[vdst + e * 16] = vv[e];
+        for (int e = 0; e < 8; ++e) v_pool[pbase + (c * 8 + e) * 16 + t] = vv[e];
+        if (v16_pool) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                v16_pool[pbase + emb::v16_index(c * 8 + e, t)] =
+                    __builtin_bit_cast(uint16_t, (_Float16)__builtin_bit_cast(float, (uint32_t)vv[e] << 16));
+        }
     }
 }
 
@@ -153,19 +163,20 @@ inline int grid_for(int64_t total) {
 
 template <typename Src>
 int launch_append(const Src *k, const Src *v, int64_t src_stride, int32_t n, const int32_t *slots,
-                  const int32_t *block_table, int32_t capacity, void *k_pool, void *v_pool, int32_t heads,
-                  int32_t head_dim, hipStream_t stream) {
+                  const int32_t *block_table, int32_t capacity, void *k_pool, void *v_pool, void *v16_pool,
+                  int32_t heads, int32_t head_dim, hipStream_t stream) {
     EMB_CHECK_ARG(k && v && slots && k_pool && v_pool, "null pointer");
     EMB_CHECK_ARG(n > 0 && heads > 0 && head_dim > 0 && capacity > 0, "non-positive size");
     EMB_CHECK_ARG(head_dim % 8 == 0, "head_dim must be a multiple of 8");
     EMB_CHECK_ARG(src_stride >= (int64_t)heads * head_dim, "src_stride smaller than a token row");
     EMB_CHECK_ARG((src_stride * (int64_t)sizeof(Src)) % 16 == 0, "source rows must be 16-byte aligned");
-    EMB_CHECK_ARG(aligned16(k) && aligned16(v) && aligned16(k_pool) && aligned16(v_pool),
+    EMB_CHECK_ARG(aligned16(k) && aligned16(v) && aligned16(k_pool) && aligned16(v_pool) && aligned16(v16_pool),
                   "buffers must be 16-byte aligned");
     MoveGeom g{n, heads, head_dim, head_dim / 8, capacity, src_stride};
     const int64_t total = (int64_t)n * heads * g.chunks;
+    EMB_CHECK_ARG(total < INT32_MAX, "append too large for one launch");
     hipLaunchKernelGGL(kv_append_kernel<Src>, dim3(grid_for(total)), dim3(256), 0, stream, k, v, slots,
-                       block_table, (uint16_t *)k_pool, (uint16_t *)v_pool, g);
+                       block_table, (uint16_t *)k_pool, (uint16_t *)v_pool, (uint16_t *)v16_pool, g);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "kv_append launch: %s", hipGetErrorString(e));
     return EMB_OK;
@@ -194,10 +205,10 @@ int launch_gather(const void *k_pool, const void *v_pool, const int32_t *valid, 
 extern "C" {
 
 int emb_kv_append(const void *k_new, const void *v_new, int64_t src_stride, int32_t n, const int32_t *slots,
-                  const int32_t *block_table, int32_t capacity, void *k_pool, void *v_pool, int32_t n_kv_heads,
-                  int32_t head_dim, hipStream_t stream) {
+                  const int32_t *block_table, int32_t capacity, void *k_pool, void *v_pool, void *v16_pool,
+                  int32_t n_kv_heads, int32_t head_dim, hipStream_t stream) {
     return launch_append<uint16_t>((const uint16_t *)k_new, (const uint16_t *)v_new, src_stride, n, slots,
-                                   block_table, capacity, k_pool, v_pool, n_kv_heads, head_dim, stream);
+                                   block_table, capacity, k_pool, v_pool, v16_pool, n_kv_heads, head_dim, stream);
 }
 
 int emb_kv_gather(const void *k_pool, const void *v_pool, const int32_t *valid, int32_t n,
@@ -215,7 +226,7 @@ int lingbot_runtime_kv_update_f32(const float *k, const float *v, float *cache_k
                                   hipStream_t stream) {
     EMB_CHECK_ARG(capacity >= 8, "capacity must be >= 8 for the bf16 paged layout");
     return launch_append<float>(k, v, (int64_t)n_heads * head_dim, seq, slots, nullptr, capacity, cache_k, cache_v,
-                                n_heads, head_dim, stream);
+                                nullptr, n_heads, head_dim, stream);
 }
 
 int lingbot_runtime_kv_gather_f32(const float *cache_k, const float *cache_v, const int *valid_slots,

@@ -11,15 +11,8 @@
 // Work decomposition.  A workgroup of 4 waves owns 128 query rows of one
 // (sequence, kv head); a row is (token, q head of the GQA group), so all query
 // heads that share a kv head also share every K/V tile the workgroup stages in
-// LDS.  Each wave owns 32 rows.  Keys stream in tiles of KT = 64 keys (32 at
-// head_dim 256).
-//
-// Pipeline.  K/V tiles are double-buffered in LDS.  While a wave computes tile
-// t from one buffer, the global loads of tile t+1 are already in flight into
-// registers, and the block-table entries of tile t+2 are being fetched; after
-// the compute the registers are converted and written to the other buffer and
-// one barrier per tile hands it over.  The page ids of a tile are the same for
-// every thread of the workgroup, so they come through scalar loads.
+// LDS.  Each wave owns 32 rows.  Keys stream in tiles of KT = 32 keys (64 at
+// head_dim 64).
 //
 // Per wave and key tile the math is done transposed, with MFMA 32x32x16:
 //   S^T[32 keys x 32 rows] = K[keys x D] . Q^T       (bf16 x bf16 -> f32)
@@ -28,8 +21,32 @@
 // accumulators all belong to the same row, the row max needs one cross-lane
 // step (lanes l and l^32), and rescaling needs no shuffles.  P and V go through
 // f16 rather than bf16 because P in bf16 (8 significant bits) alone would put
-// the mean relative error near 1.6e-3; f16 keeps it near 2e-4.  V is converted
-// bf16 -> f16 while it is staged in LDS (exact for |v| in [2^-14, 65504]).
+// the mean relative error near 1.1e-3; f16 keeps it near 2e-4.  V in f16 is
+// exact for |v| in [2^-14, 65504].
+//
+// LDS image of a key tile (one pipeline stage):
+//   K: row r (key), 16-byte chunk c (dims 8c..8c+7) at r*D + ((c ^ swz(r))*8),
+//      swz(r) = r & min(D/8 - 1, 15): the XOR keeps the 16 rows one MFMA
+//      operand read touches on distinct banks without padding.
+//   V: page p of the tile, dim d: 16 f16 keys at (p*D + d)*16, in the key
+//      order the P.V MFMA consumes (key t at position t with bits 2 and 3
+//      swapped), the two 8-key halves exchanged when bit 3 of d is set.
+// Tiles reach LDS in one of three ways:
+//   * DMA: with an f16 V shadow pool (written by the append in exactly the
+//     V image above), K rows and V pages are copied by buffer loads that write
+//     LDS directly (16 bytes a lane); no registers, no conversion.
+//   * REG: bf16 V is loaded into registers, converted to f16 and permuted,
+//     then written; K goes the same way.
+//   * VALID: like REG, but key j is the slot valid[j] of an arbitrary list.
+// Page ids come from an LDS copy of the block-table segment; each page is read
+// through a buffer resource sized to its valid rows, so the end of the key
+// list reads as zeros without branches.
+//
+// Pipeline over three LDS stages: at tile t, one stage holds tile t (its V
+// feeds P.V), one tile t+1 (its K feeds the next S) and one receives tile t+2,
+// whose loads are in flight for the whole iteration.  The S MFMAs of tile t+1
+// overlap the softmax VALU work of tile t, and the P.V MFMAs of tile t overlap
+// the staging of tile t+2.  One barrier a tile.
 //
 // The online softmax keeps the running max in raw score units and rescales
 // the accumulators only when some row's max grows by more than 2^8 in the
@@ -55,28 +72,35 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int WAVES = 4;
 constexpr int ROWS_PER_WAVE = 32;
 constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
 constexpr float RESCALE_TH = 8.0f;  // log2 units
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr int SEG_PAGES = 1024;  // block-table entries held in LDS at a time (16384 keys)
+constexpr uint32_t RSRC_W3 = 0x00020000u;  // buffer resource word 3 (raw, 32-bit elements)
+
+enum { LD_DMA = 0, LD_REG = 1, LD_VALID = 2 };
 
 template <int D>
 struct Geo {
-    // keys per tile: four pages, two at D = 256 where the accumulators and the
-    // query fragment already hold 192 registers a lane
-    static constexpr int KT = D >= 256 ? 32 : 64;
-    static constexpr int KB = KT / 32;             // 32-key MFMA blocks per tile
+    // keys per tile: two pages at D >= 128 (three stages of 32 keys fit two
+    // workgroups a CU at D = 128), four at D = 64
+    static constexpr int KT = D >= 128 ? 32 : 64;
+    static constexpr int KB = KT / 32;          // 32-key MFMA blocks per tile
     static constexpr int PAGES = KT / 16;
-    static constexpr int CH = D / 8;               // 16-byte chunks per key row
-    static constexpr int KS = D + 8;               // bf16 elements per staged K row
-    static constexpr int VS = KT + 8;              // f16 elements per staged V^T row
-    static constexpr int KPT = KT * CH / 256;      // K chunks per thread per tile
-    static constexpr int VPT = D * KT / 8 / 256;   // V chunks per thread per tile
-    static constexpr int STAGE = KT * KS + D * VS; // uint16 elements per LDS stage
+    static constexpr int CH = D / 8;            // 16-byte chunks per key row
+    static constexpr int SWZ = (CH < 16 ? CH : 16) - 1;
+    static constexpr int K_ELEMS = KT * D;      // bf16 K image
+    static constexpr int V_ELEMS = KT * D;      // f16 V image
+    static constexpr int STAGE = K_ELEMS + V_ELEMS;
+    static constexpr int BLOCKS = K_ELEMS * 2 / 1024;  // 1 KB DMA blocks per image
+    static constexpr int KPT = KT * CH / 256;   // register path: K chunks per thread
+    static constexpr int VPT = D * KT / 8 / 256;
     static constexpr int MIN_WG = D >= 256 ? 1 : 2;
-    static_assert(KPT >= 1 && VPT >= 1, "tile too small for 256 threads");
+    static_assert(KPT >= 1 && VPT >= 1 && BLOCKS % 4 == 0, "tile too small for 256 threads");
 };
 
 struct KParams {
@@ -89,6 +113,7 @@ struct KParams {
     int32_t nq_single, nk_single;  // used when cu_q / n_keys are null (batch 1)
     const uint16_t *k_pool;
     const uint16_t *v_pool;
+    const uint16_t *v16_pool;
     const int32_t *bt;
     int32_t bt_stride;
     const int32_t *valid;
@@ -131,44 +156,113 @@ __device__ __forceinline__ int32_t page_of(const int32_t *bt_b, int32_t slot) {
     return bt_b ? bt_b[slot >> 4] : (slot >> 4);
 }
 
-// Global-to-register staging of one K/V tile.
+// Element offsets inside a stage (see the header comment).
+template <int D>
+__device__ __forceinline__ int k_off(int row, int chunk) {
+    return row * D + ((chunk ^ (row & Geo<D>::SWZ)) << 3);
+}
+template <int D>
+__device__ __forceinline__ int v_off(int page, int d, int half) {
+    return Geo<D>::K_ELEMS + (page * D + d) * 16 + ((half ^ ((d >> 3) & 1)) << 3);
+}
+
+// The tile's page ids (uniform over the workgroup) from the LDS block table.
+template <int D>
+__device__ __forceinline__ void tile_pages(const int32_t *pt, int32_t (&pid)[Geo<D>::PAGES]) {
+    if constexpr (Geo<D>::PAGES == 4) {
+        const i32x4 w = *reinterpret_cast<const i32x4 *>(pt);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pid[i] = __builtin_amdgcn_readfirstlane(w[i]);
+    } else {
+        const i32x2 w = *reinterpret_cast<const i32x2 *>(pt);
+        pid[0] = __builtin_amdgcn_readfirstlane(w[0]);
+        pid[1] = __builtin_amdgcn_readfirstlane(w[1]);
+    }
+}
+
+// Tile keys k0 + [0, KT), key j = logical slot j.  Buffer resources of the
+// tile's pages: K covers only the rows below lim = min(n_keys, capacity), V
+// the whole page (nothing for an unmapped page).
+template <int D>
+__device__ __forceinline__ void page_rsrc(const KParams &p, const uint16_t *vbase, const int32_t (&pid)[Geo<D>::PAGES],
+                                          int32_t k0, int32_t lim, int32_t kvh,
+                                          __amdgpu_buffer_rsrc_t (&kr)[Geo<D>::PAGES],
+                                          __amdgpu_buffer_rsrc_t (&vr)[Geo<D>::PAGES]) {
+#pragma unroll
+    for (int pg = 0; pg < Geo<D>::PAGES; ++pg) {
+        const int32_t page = pid[pg];
+        const int32_t rows = page < 0 ? 0 : min(max(lim - (k0 + pg * 16), 0), 16);
+        const int64_t off = page < 0 ? 0 : ((int64_t)page * p.hkv + kvh) * (16 * D);
+        kr[pg] = __builtin_amdgcn_make_buffer_rsrc((void *)(p.k_pool + off), 0, rows * D * 2, RSRC_W3);
+        vr[pg] = __builtin_amdgcn_make_buffer_rsrc((void *)(vbase + off), 0, rows > 0 ? 16 * D * 2 : 0, RSRC_W3);
+    }
+}
+
+// DMA path: the tile's K rows and f16 V-shadow pages go straight into the
+// stage.  Wave w issues 1 KB blocks b = 4j + w of each image; block b of the
+// K image holds key rows [b*64/CH, (b+1)*64/CH), so lane i loads the global
+// chunk that the XOR swizzle puts at slot (b*64 + i) % CH of its row.  A block
+// never crosses a page, so one resource serves all 64 lanes.
+template <int D>
+__device__ __forceinline__ void issue_dma(const KParams &p, const int32_t *pt, int32_t k0, int32_t lim, int32_t kvh,
+                                          uint16_t *stage) {
+    using G = Geo<D>;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int32_t pid[G::PAGES];
+    tile_pages<D>(pt, pid);
+    __amdgpu_buffer_rsrc_t kr[G::PAGES], vr[G::PAGES];
+    page_rsrc<D>(p, p.v16_pool, pid, k0, lim, kvh, kr, vr);
+    constexpr int RB = 64 / G::CH;  // key rows per K block
+#pragma unroll
+    for (int j = 0; j < G::BLOCKS / 4; ++j) {
+        const int b = j * 4 + wave;
+        const int q = b * 64 + lane;
+        const int r = q / G::CH, s = q % G::CH;
+        const int c = s ^ (r & G::SWZ);
+        __amdgpu_buffer_rsrc_t rk;
+        // page of block b = (4j + w) * RB / 16: j*RB/4 for RB <= 4 (w < 4),
+        // 2j + w/2 for RB = 8 (D = 64)
+        if constexpr (RB <= 4)
+            rk = kr[(j * RB) / 4];
+        else
+            rk = (wave >> 1) ? kr[2 * j + 1] : kr[2 * j];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(stage + b * 512), 16, ((r & 15) * D + c * 8) * 2,
+                                                 0, 0, 0);
+    }
+    // V image: page pp covers blocks [pp*D/32, (pp+1)*D/32)
+#pragma unroll
+    for (int j = 0; j < G::BLOCKS / 4; ++j) {
+        const int b = j * 4 + wave;
+        __amdgpu_buffer_rsrc_t rv;
+        int pp_lo;
+        if constexpr (D >= 128) {
+            pp_lo = (j * 4 * 32) / D;
+            rv = vr[pp_lo];
+        } else {
+            pp_lo = 2 * j + (wave >> 1);
+            rv = (wave >> 1) ? vr[2 * j + 1] : vr[2 * j];
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(stage + G::K_ELEMS + b * 512), 16,
+                                                 b * 1024 - pp_lo * D * 32 + lane * 16, 0, 0, 0);
+    }
+}
+
+// Register paths: global -> registers (in flight during the compute of the
+// previous tile) -> converted and written into the stage image.
 template <int D, bool VALID>
-struct Loader {
+struct RegLoader {
     using G = Geo<D>;
     u32x4 k[G::KPT];
     u32x4 v[G::VPT];
 
-    // Keys of the tile are k0 + [0, KT).  Without a valid-slot list, key j is
-    // logical slot j, so every 8-key group of V is contiguous inside one page
-    // and the tile's KT/16 page ids (uniform over the workgroup) are all that
-    // is needed.  Each page is read through a buffer resource whose size
-    // covers only its valid rows (K) or nothing (an unmapped page), so the
-    // hardware range check returns zeros where the key list ends, without
-    // branches.  lim = min(n_keys, capacity).
     __device__ __forceinline__ void issue_direct(const KParams &p, const int32_t *pt, int32_t k0, int32_t lim,
                                                  int32_t kvh) {
         const int tid = threadIdx.x;
         int32_t pid[G::PAGES];
-        if constexpr (G::PAGES == 4) {
-            const i32x4 w = *reinterpret_cast<const i32x4 *>(pt);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pid[i] = w[i];
-        } else {
-            const i32x2 w = *reinterpret_cast<const i32x2 *>(pt);
-            pid[0] = w[0];
-            pid[1] = w[1];
-        }
+        tile_pages<D>(pt, pid);
         __amdgpu_buffer_rsrc_t kr[G::PAGES], vr[G::PAGES];
-#pragma unroll
-        for (int pg = 0; pg < G::PAGES; ++pg) {
-            const int32_t page = __builtin_amdgcn_readfirstlane(pid[pg]);
-            const int32_t first = k0 + pg * 16;
-            const int32_t rows = page < 0 ? 0 : min(max(lim - first, 0), 16);
-            const int64_t pk = page < 0 ? 0 : ((int64_t)page * p.hkv + kvh) * (16 * D);
-            kr[pg] = __builtin_amdgcn_make_buffer_rsrc((void *)(p.k_pool + pk), 0, rows * D * 2, 0x00020000);
-            vr[pg] = __builtin_amdgcn_make_buffer_rsrc((void *)(p.v_pool + pk), 0, rows > 0 ? 16 * D * 2 : 0,
-                                                       0x00020000);
-        }
+        page_rsrc<D>(p, p.v_pool, pid, k0, lim, kvh, kr, vr);
         // Page of a chunk.  A page holds 16*CH K chunks and 2*D V chunks; at
         // D >= 128 that is >= 256, so chunk i of every thread lies in page
         // i*256/(page chunks), a constant.  At D = 64 a page is 128 chunks and
@@ -268,18 +362,16 @@ struct Loader {
         }
     }
 
-    // Registers -> LDS stage: K rows as bf16; V transposed to [d][key] in f16
-    // with the key permutation the PV MFMA reads (within a 16-key page, key t
-    // sits at position t with bits 2 and 3 swapped).
+    // Registers -> stage image: K chunks to their swizzled slots; V to f16, keys
+    // +0..3 of the 8-key half to permuted positions half*4.. of image half 0,
+    // keys +4..7 to image half 1.
     __device__ __forceinline__ void store(uint16_t *stage) const {
         const int tid = threadIdx.x;
-        uint16_t *ks = stage;
-        uint16_t *vs = stage + G::KT * G::KS;
 #pragma unroll
         for (int i = 0; i < G::KPT; ++i) {
             const int c = tid + i * 256;
             const int key = c / G::CH, dc = c % G::CH;
-            *reinterpret_cast<u32x4 *>(&ks[key * G::KS + dc * 8]) = k[i];
+            *reinterpret_cast<u32x4 *>(&stage[k_off<D>(key, dc)]) = k[i];
         }
 #pragma unroll
         for (int i = 0; i < G::VPT; ++i) {
@@ -289,14 +381,11 @@ struct Loader {
             const int d = rem >> 1, half = rem & 1;
             const u32x2 lo = {bf16x2_to_f16x2(v[i][0]), bf16x2_to_f16x2(v[i][1])};  // keys +0..3
             const u32x2 hi = {bf16x2_to_f16x2(v[i][2]), bf16x2_to_f16x2(v[i][3])};  // keys +4..7
-            uint16_t *row = &vs[d * G::VS + pg * 16];
-            *reinterpret_cast<u32x2 *>(row + half * 4) = lo;
-            *reinterpret_cast<u32x2 *>(row + 8 + half * 4) = hi;
+            *reinterpret_cast<u32x2 *>(&stage[v_off<D>(pg, d, 0) + half * 4]) = lo;
+            *reinterpret_cast<u32x2 *>(&stage[v_off<D>(pg, d, 1) + half * 4]) = hi;
         }
     }
 };
-
-constexpr int SEG_PAGES = 1024;  // block-table entries held in LDS at a time (16384 keys)
 
 // pt[i] = page id of page index seg_p0 + i, or -1 at and past p_end.
 __device__ __forceinline__ void load_segment(const int32_t *bt_b, int32_t seg_p0, int32_t p_end, int32_t *pt) {
@@ -306,10 +395,11 @@ __device__ __forceinline__ void load_segment(const int32_t *bt_b, int32_t seg_p0
     }
 }
 
-template <int D, int MASK, bool VALID, bool QF32>
+template <int D, int MASK, int LD, bool QF32>
 __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams p) {
     using G = Geo<D>;
-    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * G::STAGE];
+    constexpr bool VALID = LD == LD_VALID;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[3 * G::STAGE];
     __shared__ __attribute__((aligned(16))) int32_t pt[VALID ? 4 : SEG_PAGES];
 
     // XCD-aware order: hardware ids go round-robin over the 8 XCDs, so logical
@@ -403,65 +493,88 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     for (int i = 0; i < D / 32; ++i) acc_o[i] = f32x16{};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    Loader<D, VALID> ld;
     const int32_t lim = min(nk, p.capacity);  // slots at or past the capacity are zero rows
     const int32_t p_end = (min(lim, t_hi * G::KT) + 15) / 16;
     int32_t seg_p0 = t_lo * G::PAGES;
-    if (t_lo < t_hi) {
-        if (VALID) {
-            ld.issue_valid(p, valid_b, bt_b, t_lo * G::KT, nk, kvh);
+
+    // Starts the transfer of tile tt into stage st (a uniform call: every
+    // thread of the workgroup reaches it).  DMA writes the stage directly;
+    // the register paths fill l, which finish() writes out.  The direct paths
+    // read page ids from the LDS copy of the block table, reloading the next
+    // segment when tt leaves it (every wave is past its last read of the old
+    // one: the previous tile ended with a barrier).
+    auto issue = [&](RegLoader<D, VALID> &l, int32_t tt, uint16_t *st) {
+        if constexpr (LD == LD_VALID) {
+            l.issue_valid(p, valid_b, bt_b, tt * G::KT, nk, kvh);
         } else {
-            load_segment(bt_b, seg_p0, p_end, pt);
-            __syncthreads();
-            ld.issue_direct(p, pt, t_lo * G::KT, lim, kvh);
-        }
-        ld.store(smem);
-        __syncthreads();
-    }
-    // Every load issued so far (the query fragment included) has landed.
-    // Without this the compiler, merging the path that skips the prologue,
-    // treats the query registers as possibly in flight inside the loop and
-    // waits for all outstanding loads -- the next tile's prefetch included --
-    // before the first MFMA of every tile.
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-
-    for (int32_t t = t_lo; t < t_hi; ++t) {
-        const int32_t k0 = t * G::KT;
-        const bool more = t + 1 < t_hi;
-        const uint16_t *cur = smem + ((t - t_lo) & 1) * G::STAGE;
-        uint16_t *nxt = smem + ((t - t_lo + 1) & 1) * G::STAGE;
-
-        // (1) loads of tile t+1 in flight during the compute of tile t
-        if (more) {
-            if (VALID) {
-                ld.issue_valid(p, valid_b, bt_b, k0 + G::KT, nk, kvh);
-            } else {
-                int32_t pi = (t + 1) * G::PAGES - seg_p0;
-                if (pi + G::PAGES > SEG_PAGES) {  // next block-table segment (every wave is past its last read)
-                    seg_p0 = (t + 1) * G::PAGES;
-                    load_segment(bt_b, seg_p0, p_end, pt);
-                    __syncthreads();
-                    pi = 0;
-                }
-                ld.issue_direct(p, pt + pi, k0 + G::KT, lim, kvh);
+            int32_t pi = tt * G::PAGES - seg_p0;
+            if (pi + G::PAGES > SEG_PAGES) {
+                seg_p0 = tt * G::PAGES;
+                load_segment(bt_b, seg_p0, p_end, pt);
+                __syncthreads();
+                pi = 0;
             }
+            if constexpr (LD == LD_DMA)
+                issue_dma<D>(p, pt + pi, tt * G::KT, lim, kvh, st);
+            else
+                l.issue_direct(p, pt + pi, tt * G::KT, lim, kvh);
         }
+    };
+    auto finish = [&](const RegLoader<D, VALID> &l, uint16_t *st) {
+        if constexpr (LD == LD_DMA)
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this thread's LDS-bound loads landed
+        else
+            l.store(st);
+    };
 
-        // (2) S^T = K Q^T : in block kb, lane holds keys kb*32 + (r/4)*8 + lhi*4 + r%4 of row lrow.
-        const uint16_t *ks = cur;
-        const uint16_t *vs = cur + G::KT * G::KS;
-        f32x16 s[G::KB];
+    // S^T = K Q^T of the tile in stage st: in block kb, lane holds keys
+    // kb*32 + (r/4)*8 + lhi*4 + r%4 of row lrow.
+    auto qk = [&](const uint16_t *st, f32x16(&s)[G::KB]) {
 #pragma unroll
         for (int kb = 0; kb < G::KB; ++kb) {
             s[kb] = f32x16{};
 #pragma unroll
             for (int kk = 0; kk < D / 16; ++kk) {
-                const u32x4 kw = *reinterpret_cast<const u32x4 *>(&ks[(kb * 32 + lrow) * G::KS + kk * 16 + lhi * 8]);
+                const u32x4 kw = *reinterpret_cast<const u32x4 *>(&st[k_off<D>(kb * 32 + lrow, kk * 2 + lhi)]);
                 s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kw), qf[kk], s[kb], 0, 0, 0);
             }
         }
+    };
 
-        // (3) mask (raw score units), tile max
+    // Prologue: tiles t_lo and t_lo+1 staged, S of tile t_lo computed.
+    RegLoader<D, VALID> ld;
+    if (t_lo < t_hi) {
+        if (LD != LD_VALID) {
+            load_segment(bt_b, seg_p0, p_end, pt);
+            __syncthreads();
+        }
+        RegLoader<D, VALID> l1;
+        issue(ld, t_lo, smem);
+        if (t_lo + 1 < t_hi) issue(l1, t_lo + 1, smem + G::STAGE);
+        finish(ld, smem);
+        if (t_lo + 1 < t_hi) finish(l1, smem + G::STAGE);
+        __syncthreads();
+    }
+    // Every load issued so far (the query fragment included) has landed.
+    // Without this the compiler, merging the path that skips the prologue,
+    // treats the query registers as possibly in flight inside the loop and
+    // waits for all outstanding loads -- the prefetch included -- before the
+    // first MFMA of every tile.
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    f32x16 s_cur[G::KB];
+    qk(smem, s_cur);
+
+    // Stage `cur` holds tile t, nx1 tile t+1, nx2 receives tile t+2.  Past the
+    // end, the extra S and the stores work on stale stage contents that
+    // nothing reads.
+    int cur = 0;
+    for (int32_t t = t_lo; t < t_hi; ++t) {
+        const int32_t k0 = t * G::KT;
+        const int nx1 = cur == 2 ? 0 : cur + 1;
+        const int nx2 = nx1 == 2 ? 0 : nx1 + 1;
+        if (t + 2 < t_hi) issue(ld, t + 2, smem + nx2 * G::STAGE);
+
+        // mask (raw score units) and row max of tile t
         bool tile_full = k0 + G::KT <= nk;
         if (MASK == EMB_MASK_CHUNK) tile_full = tile_full && k0 >= full_lo && k0 + G::KT <= full_hi;
         if (MASK == EMB_MASK_TOKEN || MASK == EMB_MASK_ADD || MASK == EMB_MASK_BLOCKMAP) tile_full = false;
@@ -470,7 +583,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             for (int kb = 0; kb < G::KB; ++kb) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    float x = s[kb][r];
+                    float x = s_cur[kb][r];
                     const int32_t j = k0 + kb * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
                     bool vis = row_ok && j < nk;
                     if (MASK == EMB_MASK_CHUNK) {
@@ -490,7 +603,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                             vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
                                                                             (int64_t)tok * p.mask_q_stride + j] != 0;
                     }
-                    s[kb][r] = vis ? x : -INFINITY;
+                    s_cur[kb][r] = vis ? x : -INFINITY;
                 }
             }
         }
@@ -498,9 +611,9 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
 #pragma unroll
         for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s_cur[kb][r]);
         mt = fmaxf(mt, __shfl_xor(mt, 32));
-        // (4) wave-uniform lazy rescale
+        // wave-uniform lazy rescale
         if (__builtin_amdgcn_ballot_w64(mt > m_run + p.th_raw) != 0) {
             const float m_new = fmaxf(m_run, mt);
             const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
@@ -509,35 +622,40 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             l_run *= alpha;
             m_run = m_new;
         }
+
+        // S of tile t+1 (MFMA) alongside P of tile t (VALU)
+        f32x16 s_nxt[G::KB];
+        qk(smem + nx1 * G::STAGE, s_nxt);
         const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * p.c_log2;
         f16x8 pf[G::KB][2];
 #pragma unroll
         for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], p.c_log2, neg_mc));
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][r], p.c_log2, neg_mc));
                 l_run += e;
                 pf[kb][r >> 3][r & 7] = (_Float16)e;
             }
 
-        // (5) O^T += V^T P^T, one 16-key page per MFMA step.
+        // O^T += V^T P^T of tile t (MFMA, one 16-key page a step) alongside the
+        // staging of tile t+2
+        const uint16_t *st = smem + cur * G::STAGE;
 #pragma unroll
         for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
             for (int pg = 0; pg < 2; ++pg)
 #pragma unroll
                 for (int dt = 0; dt < D / 32; ++dt) {
-                    const u32x4 vw = *reinterpret_cast<const u32x4 *>(
-                        &vs[(dt * 32 + lrow) * G::VS + kb * 32 + pg * 16 + lhi * 8]);
+                    const u32x4 vw = *reinterpret_cast<const u32x4 *>(&st[v_off<D>(kb * 2 + pg, dt * 32 + lrow, lhi)]);
                     acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vw), pf[kb][pg],
                                                                       acc_o[dt], 0, 0, 0);
                 }
-
-        // (6) hand tile t+1 over through the other LDS stage
-        if (more) ld.store(nxt);
+        finish(ld, smem + nx2 * G::STAGE);
         __syncthreads();
+#pragma unroll
+        for (int kb = 0; kb < G::KB; ++kb) s_cur[kb] = s_nxt[kb];
+        cur = nx1;
     }
-
     l_run += __shfl_xor(l_run, 32);
     if (!row_ok) return;
 
@@ -609,27 +727,34 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
     }
 }
 
-template <int D, int MASK, bool VALID, bool QF32>
+template <int D, int MASK, int LD, bool QF32>
 hipError_t launch_kernel(const KParams &kp, hipStream_t stream) {
     const int grid = (kp.total_wg + 7) / 8 * 8;
-    hipLaunchKernelGGL((paged_attn_kernel<D, MASK, VALID, QF32>), dim3(grid), dim3(256), 0, stream, kp);
+    hipLaunchKernelGGL((paged_attn_kernel<D, MASK, LD, QF32>), dim3(grid), dim3(256), 0, stream, kp);
     return hipGetLastError();
 }
 
 template <int D, int MASK>
-hipError_t dispatch_vq(const KParams &kp, bool valid, bool qf32, hipStream_t stream) {
-    if (valid) return qf32 ? launch_kernel<D, MASK, true, true>(kp, stream) : launch_kernel<D, MASK, true, false>(kp, stream);
-    return qf32 ? launch_kernel<D, MASK, false, true>(kp, stream) : launch_kernel<D, MASK, false, false>(kp, stream);
+hipError_t dispatch_lq(const KParams &kp, int ld, bool qf32, hipStream_t stream) {
+    switch (ld) {
+        case LD_DMA:
+            return qf32 ? launch_kernel<D, MASK, LD_DMA, true>(kp, stream) : launch_kernel<D, MASK, LD_DMA, false>(kp, stream);
+        case LD_REG:
+            return qf32 ? launch_kernel<D, MASK, LD_REG, true>(kp, stream) : launch_kernel<D, MASK, LD_REG, false>(kp, stream);
+        default:
+            return qf32 ? launch_kernel<D, MASK, LD_VALID, true>(kp, stream)
+                        : launch_kernel<D, MASK, LD_VALID, false>(kp, stream);
+    }
 }
 
 template <int D>
-hipError_t dispatch_mask(const KParams &kp, int mask, bool valid, bool qf32, hipStream_t stream) {
+hipError_t dispatch_mask(const KParams &kp, int mask, int ld, bool qf32, hipStream_t stream) {
     switch (mask) {
-        case EMB_MASK_FULL: return dispatch_vq<D, EMB_MASK_FULL>(kp, valid, qf32, stream);
-        case EMB_MASK_CHUNK: return dispatch_vq<D, EMB_MASK_CHUNK>(kp, valid, qf32, stream);
-        case EMB_MASK_TOKEN: return dispatch_vq<D, EMB_MASK_TOKEN>(kp, valid, qf32, stream);
-        case EMB_MASK_ADD: return dispatch_vq<D, EMB_MASK_ADD>(kp, valid, qf32, stream);
-        default: return dispatch_vq<D, EMB_MASK_BLOCKMAP>(kp, valid, qf32, stream);
+        case EMB_MASK_FULL: return dispatch_lq<D, EMB_MASK_FULL>(kp, ld, qf32, stream);
+        case EMB_MASK_CHUNK: return dispatch_lq<D, EMB_MASK_CHUNK>(kp, ld, qf32, stream);
+        case EMB_MASK_TOKEN: return dispatch_lq<D, EMB_MASK_TOKEN>(kp, ld, qf32, stream);
+        case EMB_MASK_ADD: return dispatch_lq<D, EMB_MASK_ADD>(kp, ld, qf32, stream);
+        default: return dispatch_lq<D, EMB_MASK_BLOCKMAP>(kp, ld, qf32, stream);
     }
 }
 
@@ -660,7 +785,8 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     EMB_CHECK_ARG(a->q_stride >= (int64_t)a->hq * a->head_dim && (a->q_stride * esz) % 16 == 0,
                   "q_stride must cover a token and keep 16-byte alignment");
     EMB_CHECK_ARG(a->out_stride >= (int64_t)a->hq * a->head_dim && a->out_stride % 4 == 0, "bad out_stride");
-    EMB_CHECK_ARG(aligned16(a->q) && aligned16(a->out) && aligned16(a->k_pool) && aligned16(a->v_pool),
+    EMB_CHECK_ARG(aligned16(a->q) && aligned16(a->out) && aligned16(a->k_pool) && aligned16(a->v_pool) &&
+                      aligned16(a->v16_pool),
                   "buffers must be 16-byte aligned");
     EMB_CHECK_ARG(a->mask_kind >= EMB_MASK_FULL && a->mask_kind <= EMB_MASK_BLOCKMAP, "unknown mask kind");
     if (a->mask_kind == EMB_MASK_CHUNK) EMB_CHECK_ARG(a->chunk > 0, "chunk must be positive");
@@ -683,6 +809,7 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     kp.nk_single = nk_single;
     kp.k_pool = (const uint16_t *)a->k_pool;
     kp.v_pool = (const uint16_t *)a->v_pool;
+    kp.v16_pool = (const uint16_t *)a->v16_pool;
     kp.bt = a->block_tables;
     kp.bt_stride = a->bt_stride;
     kp.valid = a->valid_slots;
@@ -714,13 +841,13 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
         kp.ws_o = (float *)a->workspace;
         kp.ws_ml = kp.ws_o + rows_all * a->head_dim;
     }
-    const bool valid = a->valid_slots != nullptr;
+    const int ld = a->valid_slots ? LD_VALID : (a->v16_pool ? LD_DMA : LD_REG);
     const bool qf32 = a->q_is_f32 != 0;
     hipError_t e;
     switch (a->head_dim) {
-        case 64: e = dispatch_mask<64>(kp, a->mask_kind, valid, qf32, stream); break;
-        case 128: e = dispatch_mask<128>(kp, a->mask_kind, valid, qf32, stream); break;
-        default: e = dispatch_mask<256>(kp, a->mask_kind, valid, qf32, stream); break;
+        case 64: e = dispatch_mask<64>(kp, a->mask_kind, ld, qf32, stream); break;
+        case 128: e = dispatch_mask<128>(kp, a->mask_kind, ld, qf32, stream); break;
+        default: e = dispatch_mask<256>(kp, a->mask_kind, ld, qf32, stream); break;
     }
     if (e == hipSuccess && splits > 1) {
         switch (a->head_dim) {

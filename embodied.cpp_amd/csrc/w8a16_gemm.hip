@@ -36,7 +36,8 @@
 // [0, n_q) go to a bf16 Q buffer, the next n_kv to the K pages and the last
 // n_kv to the V pages of a paged KV pool (emb_kv.h layout), at logical slot
 // slots[m] of the token -- the append of runtime_kv_update (kernels/lingbot/
-// lingbot_flex_attn_cuda.cu:626-649) fused into the projection.
+// lingbot_flex_attn_cuda.cu:626-649) fused into the projection, and the f16 V
+// shadow when one is given.
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -70,7 +71,7 @@ struct GParams {
     int32_t n_q, n_kv, head_dim, hkv, capacity;
     const int32_t *slots;
     const int32_t *bt;
-    uint16_t *k_pool, *v_pool;
+    uint16_t *k_pool, *v_pool, *v16_pool;
 };
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
@@ -295,12 +296,15 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
                             const bool is_v = c >= p.n_kv;
                             const int32_t cc = is_v ? c - p.n_kv : c;
                             const int32_t h = cc / p.head_dim, d = cc % p.head_dim;
-                            if (!is_v)
-                                p.k_pool[(((int64_t)page * p.hkv + h) * 16 + (slot & 15)) * p.head_dim + d] =
-                                    (uint16_t)bits;
-                            else
-                                p.v_pool[(((int64_t)page * p.hkv + h) * p.head_dim + d) * 16 + (slot & 15)] =
-                                    (uint16_t)bits;
+                            const int64_t pbase = ((int64_t)page * p.hkv + h) * 16 * p.head_dim;
+                            if (!is_v) {
+                                p.k_pool[pbase + (slot & 15) * p.head_dim + d] = (uint16_t)bits;
+                            } else {
+                                p.v_pool[pbase + d * 16 + (slot & 15)] = (uint16_t)bits;
+                                if (p.v16_pool)
+                                    p.v16_pool[pbase + emb::v16_index(d, slot & 15)] = __builtin_bit_cast(
+                                        uint16_t, (_Float16)__builtin_bit_cast(float, bits << 16));
+                            }
                         }
                     }
                 }
@@ -391,7 +395,7 @@ int emb_w8a16_gemm(const void *x, int32_t x_is_f32, int64_t ldx, const int32_t *
 int emb_w8a16_qkv_append(const void *x, int32_t x_is_f32, int64_t ldx, const int32_t *qweight,
                          const uint16_t *scales, int32_t M, int32_t K, int32_t n_q, void *q_out, int64_t ldq,
                          const int32_t *slots, const int32_t *block_table, int32_t capacity, void *k_pool,
-                         void *v_pool, int32_t n_kv_heads, int32_t head_dim, hipStream_t stream) {
+                         void *v_pool, void *v16_pool, int32_t n_kv_heads, int32_t head_dim, hipStream_t stream) {
     EMB_CHECK_ARG(slots && k_pool && v_pool, "null slots/pool");
     EMB_CHECK_ARG(n_q >= 0 && n_kv_heads > 0 && head_dim > 0 && capacity > 0, "bad sizes");
     EMB_CHECK_ARG(n_q == 0 || (q_out && ldq >= n_q), "q_out and ldq >= n_q required when n_q > 0");
@@ -414,6 +418,7 @@ int emb_w8a16_qkv_append(const void *x, int32_t x_is_f32, int64_t ldx, const int
     p.bt = block_table;
     p.k_pool = (uint16_t *)k_pool;
     p.v_pool = (uint16_t *)v_pool;
+    p.v16_pool = (uint16_t *)v16_pool;
     return run_gemm(p, x_is_f32 != 0, Y_QKV, stream);
 }
 

@@ -31,7 +31,7 @@ class AttnArgs(C.Structure):
         ("q", vp), ("q_is_f32", C.c_int32), ("q_stride", C.c_int64),
         ("out", vp), ("out_stride", C.c_int64),
         ("cu_q", vp), ("n_keys", vp), ("q_pos0", vp),
-        ("k_pool", vp), ("v_pool", vp),
+        ("k_pool", vp), ("v_pool", vp), ("v16_pool", vp),
         ("block_tables", vp), ("bt_stride", C.c_int32),
         ("valid_slots", vp), ("valid_stride", C.c_int32),
         ("capacity", C.c_int32), ("batch", C.c_int32), ("hq", C.c_int32), ("hkv", C.c_int32),
@@ -78,7 +78,7 @@ _SIGS = {
     "emb_self_block_table": (C.c_int64, [vp, i32p, i32p]),
     "emb_cross_block_table": (C.c_int64, [vp, i32p, i32p]),
     "emb_self_token_mask": (C.c_int, [vp, u8p]),
-    "emb_kv_append": (C.c_int, [vp, vp, C.c_int64, C.c_int32, vp, vp, C.c_int32, vp, vp,
+    "emb_kv_append": (C.c_int, [vp, vp, C.c_int64, C.c_int32, vp, vp, C.c_int32, vp, vp, vp,
                                 C.c_int32, C.c_int32, vp]),
     "emb_kv_gather": (C.c_int, [vp, vp, vp, C.c_int32, vp, C.c_int32, vp, vp, C.c_int32,
                                 C.c_int32, vp]),
@@ -100,7 +100,7 @@ _SIGS = {
     "emb_w8a16_gemm": (C.c_int, [vp, C.c_int32, C.c_int64, vp, vp, C.c_int32, C.c_int32, C.c_int32,
                                  vp, C.c_int64, C.c_int32, vp]),
     "emb_w8a16_qkv_append": (C.c_int, [vp, C.c_int32, C.c_int64, vp, vp, C.c_int32, C.c_int32,
-                                       C.c_int32, vp, C.c_int64, vp, vp, C.c_int32, vp, vp,
+                                       C.c_int32, vp, C.c_int64, vp, vp, C.c_int32, vp, vp, vp,
                                        C.c_int32, C.c_int32, vp]),
     "cosmos3_w8a16_linear_f32": (C.c_int, [vp, vp, vp, vp] + [C.c_int] * 7 + [vp]),
     "cosmos3_w8a16_linear_f32_ws": (C.c_int, [vp] * 8 + [C.c_int] * 7 + [vp]),
@@ -273,10 +273,10 @@ def synth_normal_bf16(seed: int, n: int) -> np.ndarray:
 
 
 def kv_append(k_new, v_new, src_stride, n, slots, block_table, capacity, k_pool, v_pool, hkv, d,
-              stream=None):
+              stream=None, v16_pool=None):
     return check(lib().emb_kv_append(ptr(k_new), ptr(v_new), src_stride, n, ptr(slots),
-                                     ptr(block_table), capacity, ptr(k_pool), ptr(v_pool), hkv, d,
-                                     stream_ptr(stream)), "emb_kv_append")
+                                     ptr(block_table), capacity, ptr(k_pool), ptr(v_pool),
+                                     ptr(v16_pool), hkv, d, stream_ptr(stream)), "emb_kv_append")
 
 
 def kv_gather(k_pool, v_pool, valid, n, block_table, capacity, k_out, v_out, hkv, d, stream=None):
@@ -293,11 +293,11 @@ def w8a16_gemm(x, qweight, scales, M, K, N, y, y_kind=EMB_W8_Y_BF16, x_is_f32=Fa
 
 
 def w8a16_qkv_append(x, qweight, scales, M, K, n_q, q_out, slots, block_table, capacity, k_pool,
-                     v_pool, hkv, d, x_is_f32=False, ldx=None, ldq=None, stream=None):
+                     v_pool, hkv, d, x_is_f32=False, ldx=None, ldq=None, stream=None, v16_pool=None):
     return check(lib().emb_w8a16_qkv_append(ptr(x), int(x_is_f32), ldx or K, ptr(qweight),
                                             ptr(scales), M, K, n_q, ptr(q_out), ldq or n_q,
                                             ptr(slots), ptr(block_table), capacity, ptr(k_pool),
-                                            ptr(v_pool), hkv, d, stream_ptr(stream)),
+                                            ptr(v_pool), ptr(v16_pool), hkv, d, stream_ptr(stream)),
                  "emb_w8a16_qkv_append")
 
 
@@ -305,7 +305,7 @@ def attn_workspace_bytes(batch, max_q, hq, hkv, d, splits):
     return lib().emb_attn_workspace_bytes(batch, max_q, hq, hkv, d, splits)
 
 
-def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, capacity,
+def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, capacity, v16_pool=None,
                     cu_q=None, n_keys=None, q_pos0=None, q_is_f32=False, q_stride=None,
                     out_stride=None, block_tables=None, bt_stride=0, valid_slots=None,
                     valid_stride=0, mask_kind=EMB_MASK_FULL, chunk=0, window=-1, mask=None,
@@ -317,7 +317,7 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
     a.q_stride = q_stride if q_stride is not None else hq * d
     a.out = ptr(out); a.out_stride = out_stride if out_stride is not None else hq * d
     a.cu_q = ptr(cu_q); a.n_keys = ptr(n_keys); a.q_pos0 = ptr(q_pos0)
-    a.k_pool = ptr(k_pool); a.v_pool = ptr(v_pool)
+    a.k_pool = ptr(k_pool); a.v_pool = ptr(v_pool); a.v16_pool = ptr(v16_pool)
     a.block_tables = ptr(block_tables); a.bt_stride = bt_stride
     a.valid_slots = ptr(valid_slots); a.valid_stride = valid_stride
     a.capacity = capacity; a.batch = batch; a.hq = hq; a.hkv = hkv; a.head_dim = d

@@ -17,6 +17,15 @@
  *   V page p, kv head h, dim d, slot row t : v_pool[((p*H + h)*D + d)*16 + t]
  * A sequence's logical slot s lives in page block_table[s / 16], row s % 16;
  * block_table == NULL means the identity map (page = s / 16).
+ *
+ * Optional f16 V shadow (same page count and element count as v_pool): page
+ * p, head h, dim d holds the 16 keys of the page as f16 in the order the
+ * attention MFMA reads them,
+ *   v16_pool[((p*H + h)*D + d)*16 + (((P(t) >> 3) ^ ((d >> 3) & 1)) << 3) + (P(t) & 7)]
+ * where P(t) is row t with bits 2 and 3 swapped.  The append writes it when
+ * given; attention given one copies its pages into LDS as they are.  The bf16
+ * pool stays the bit-exact store (gather reads it).  A shadow must start
+ * zero-filled (rows never appended are read, multiplied by zero weights).
  */
 #ifndef EMB_KV_H
 #define EMB_KV_H
@@ -124,11 +133,11 @@ int emb_self_token_mask(const emb_flex_meta *m, uint8_t *mask);                /
  * k_new/v_new: bf16 rows of n_kv_heads*head_dim elements, row stride src_stride
  * (elements).  slots: int32 [n] logical slots (device); a slot outside
  * [0, capacity) or on an unmapped page (-1) is skipped, as the reference skips
- * out-of-range slots. */
+ * out-of-range slots.  v16_pool (may be NULL): the f16 V shadow, written too. */
 int emb_kv_append(const void *k_new, const void *v_new, int64_t src_stride, int32_t n,
                   const int32_t *slots, const int32_t *block_table, int32_t capacity,
-                  void *k_pool, void *v_pool, int32_t n_kv_heads, int32_t head_dim,
-                  hipStream_t stream);
+                  void *k_pool, void *v_pool, void *v16_pool, int32_t n_kv_heads,
+                  int32_t head_dim, hipStream_t stream);
 
 /* Gather rows valid[0..n) into compact [n][H][D] bf16 (reference layout):
  * runtime_kv_gather (a10, :875-898).  Out-of-range slots leave the row as is. */
@@ -163,8 +172,10 @@ typedef struct emb_attn_args {
     const int32_t *n_keys;     /* device [batch]: keys per sequence */
     const int32_t *q_pos0;     /* device [batch] or NULL: position of query 0 in
                                   key index space (NULL: n_keys - n_q) */
-    /* pool */
+    /* pool; v16_pool (may be NULL) is the f16 V shadow: when given (and no
+     * valid-slot list), tiles are copied into LDS without conversion */
     const void *k_pool, *v_pool;
+    const void *v16_pool;
     const int32_t *block_tables; /* device [batch][bt_stride] or NULL (identity) */
     int32_t bt_stride;
     const int32_t *valid_slots;  /* device [batch][valid_stride] or NULL: key j is
@@ -259,8 +270,8 @@ int emb_w8a16_gemm(const void *x, int32_t x_is_f32, int64_t ldx, const int32_t *
 int emb_w8a16_qkv_append(const void *x, int32_t x_is_f32, int64_t ldx, const int32_t *qweight,
                          const uint16_t *scales, int32_t M, int32_t K, int32_t n_q, void *q_out,
                          int64_t ldq, const int32_t *slots, const int32_t *block_table,
-                         int32_t capacity, void *k_pool, void *v_pool, int32_t n_kv_heads,
-                         int32_t head_dim, hipStream_t stream);
+                         int32_t capacity, void *k_pool, void *v_pool, void *v16_pool,
+                         int32_t n_kv_heads, int32_t head_dim, hipStream_t stream);
 
 /* Reference-named W8 face (kernels/cosmos3/cosmos3_w8_marlin_cuda.h:24-84 with
  * hipStream_t).  y is f32 holding the bf16-rounded result.  The workspaces of

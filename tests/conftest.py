@@ -34,6 +34,21 @@ def emb():
     return embkv
 
 
+def v16_shadow(v_pool: np.ndarray, d: int) -> np.ndarray:
+    """f16 V shadow of a bf16 V pool (uint16 bits, [pages*H][d][16] rows), as
+    include/emb_kv.h specifies it: row t of dim d at position P = t with bits 2
+    and 3 swapped, the two 8-key halves exchanged when bit 3 of d is set."""
+    v = v_pool.reshape(-1, d, 16)
+    f = (v.astype(np.uint32) << 16).view(np.float32).astype(np.float16).view(np.uint16)
+    t = np.arange(16)
+    P = (t & 3) | ((t >> 1) & 4) | ((t << 1) & 8)
+    dd = np.arange(d)[:, None]
+    pos = (((P[None, :] >> 3) ^ ((dd >> 3) & 1)) << 3) + (P[None, :] & 7)  # [d][16]
+    out = np.zeros_like(f)
+    out[:, dd, pos] = f[:, dd, np.broadcast_to(t, (d, 16))]
+    return out.reshape(-1)
+
+
 def rel_err(a: np.ndarray, b: np.ndarray) -> tuple[float, float]:
     """(max |a-b|, sum|a-b| / sum|b|) -- mean-rel is the relative L1 error."""
     a = np.asarray(a, np.float64)

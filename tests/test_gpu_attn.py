@@ -12,7 +12,7 @@ import math
 import numpy as np
 import pytest
 
-from conftest import assert_close
+from conftest import assert_close, v16_shadow
 
 pytestmark = pytest.mark.gpu
 
@@ -65,20 +65,29 @@ class Seqs:
         self.cu_q = np.concatenate([[0], np.cumsum(n_q)]).astype(np.int32)
 
     def run(self, emb, torch, dev, scale, splits=1, **kw):
-        out = torch.full((int(self.cu_q[-1]), self.hq, self.d), float("nan"), dtype=torch.float32, device=dev)
+        """Runs the attention twice -- tiles staged through registers from the bf16
+        V pool, and copied into LDS from the f16 V shadow -- and requires the two
+        to agree bit for bit (same arithmetic, same conversions)."""
         ws = None
         if splits > 1:
             nb = emb.attn_workspace_bytes(len(self.n_q), max(self.n_q), self.hq, self.hkv, self.d, splits)
             ws = torch.empty(nb // 4 + 4, dtype=torch.float32, device=dev)
         keep = dict(q=_t(torch, dev, np.concatenate(self.q)), kp=_t(torch, dev, self.kp),
-                    vp=_t(torch, dev, self.vp), bt=_t(torch, dev, self.bt), cu=_t(torch, dev, self.cu_q),
+                    vp=_t(torch, dev, self.vp), v16=_t(torch, dev, v16_shadow(self.vp, self.d)),
+                    bt=_t(torch, dev, self.bt), cu=_t(torch, dev, self.cu_q),
                     nk=_t(torch, dev, np.array(self.n_keys, np.int32)))
-        emb.paged_attention(q=keep["q"], out=out, k_pool=keep["kp"], v_pool=keep["vp"], batch=len(self.n_q),
-                            hq=self.hq, hkv=self.hkv, d=self.d, max_q=max(self.n_q), scale=scale,
-                            capacity=self.cap, cu_q=keep["cu"], n_keys=keep["nk"], block_tables=keep["bt"],
-                            bt_stride=self.bt_stride, splits=splits, workspace=ws, **kw)
-        torch.cuda.synchronize()
-        o = out.cpu().numpy()
+        outs = []
+        for v16 in (None, keep["v16"]):
+            out = torch.full((int(self.cu_q[-1]), self.hq, self.d), float("nan"), dtype=torch.float32, device=dev)
+            emb.paged_attention(q=keep["q"], out=out, k_pool=keep["kp"], v_pool=keep["vp"], v16_pool=v16,
+                                batch=len(self.n_q), hq=self.hq, hkv=self.hkv, d=self.d, max_q=max(self.n_q),
+                                scale=scale, capacity=self.cap, cu_q=keep["cu"], n_keys=keep["nk"],
+                                block_tables=keep["bt"], bt_stride=self.bt_stride, splits=splits, workspace=ws,
+                                **kw)
+            torch.cuda.synchronize()
+            outs.append(out.cpu().numpy())
+        assert np.array_equal(outs[0], outs[1], equal_nan=True), "register and LDS-copy paths differ"
+        o = outs[1]
         return [o[self.cu_q[b]:self.cu_q[b + 1]] for b in range(len(self.n_q))]
 
     def oracle(self, orc, b, scale, rows=None, **kw):

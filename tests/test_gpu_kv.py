@@ -6,6 +6,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+from conftest import v16_shadow
+
 pytestmark = pytest.mark.gpu
 
 
@@ -46,12 +48,19 @@ def test_append_gather_bit_exact(emb, orc, torch_dev, H, D, extra):
     # oracle
     kp_ref, vp_ref = kp0.copy(), vp0.copy()
     orc.paged_append(k, v, stride, slots, bt, H, D, cap, kp_ref, vp_ref)
-    # device
+    # device, with the f16 V shadow written alongside
     kp, vpl = _t(torch, dev, kp0), _t(torch, dev, vp0)
+    v16 = _t(torch, dev, v16_shadow(vp0, D))
     emb.kv_append(_t(torch, dev, k), _t(torch, dev, v), stride, n, _t(torch, dev, slots),
-                  _t(torch, dev, bt), cap, kp, vpl, H, D)
+                  _t(torch, dev, bt), cap, kp, vpl, H, D, v16_pool=v16)
     torch.cuda.synchronize()
     assert np.array_equal(_np(kp), kp_ref) and np.array_equal(_np(vpl), vp_ref)
+    # shadow = f16 of the bf16 pool in the documented order (NaN sources: payloads not compared)
+    exp16 = v16_shadow(vp_ref, D)
+    src_nan = np.isnan(v16_shadow(vp_ref, D).view(np.float16))
+    got16 = _np(v16)
+    assert np.array_equal(got16[~src_nan], exp16[~src_nan]), "V shadow differs"
+    assert np.isnan(got16.view(np.float16)[src_nan]).all()
     # gather: valid list in arbitrary order with out-of-range entries
     valid = np.concatenate([rng.permutation(slots[(slots >= 0) & (slots < cap)]), [-1, cap, 7]]).astype(np.int32)
     gk0 = rng.integers(0, 65536, (len(valid), H, D), dtype=np.uint16)

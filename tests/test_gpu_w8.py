@@ -22,7 +22,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import assert_close
+from conftest import assert_close, v16_shadow
 
 pytestmark = pytest.mark.gpu
 
@@ -195,8 +195,9 @@ def test_w8_qkv_append_matches_gemm(emb, orc, torch_dev):
     x_d, q_d, s_d = _t(torch, dev, x), _t(torch, dev, q), _t(torch, dev, s_st)
     kp, vp = _t(torch, dev, kp0), _t(torch, dev, vp0)
     qo = torch.zeros((M, n_q), dtype=torch.int16, device=dev)
+    v16 = _t(torch, dev, v16_shadow(vp0, d))
     emb.w8a16_qkv_append(x_d, q_d, s_d, M, K, n_q, qo, _t(torch, dev, slots), _t(torch, dev, bt), cap, kp, vp,
-                         hkv, d)
+                         hkv, d, v16_pool=v16)
     torch.cuda.synchronize()
     yb = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_BF16)
     assert np.array_equal(qo.cpu().numpy().view(np.uint16), yb[:, :n_q])
@@ -207,6 +208,7 @@ def test_w8_qkv_append_matches_gemm(emb, orc, torch_dev):
     orc.paged_append(kcols, vcols, n_kv, slots, bt, hkv, d, cap, kexp, vexp)
     assert np.array_equal(kp.cpu().numpy().view(np.uint16), kexp), "K pages differ"
     assert np.array_equal(vp.cpu().numpy().view(np.uint16), vexp), "V pages differ"
+    assert np.array_equal(v16.cpu().numpy().view(np.uint16), v16_shadow(vexp, d)), "V shadow differs"
     # and the bf16 GEMM itself is within the bf16 bar of the oracle
     yb_ref, _ = orc.w8a16_gemm(x, q, s_st, M, K, N)
     _check_bf16(yb, yb_ref, "qkv gemm", orc)

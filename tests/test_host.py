@@ -145,11 +145,18 @@ def test_synthetic_generator_matches_oracle(emb, orc):
 def test_device_entry_points_reject_bad_arguments(emb):
     L = emb.lib()
     # every check below returns before any HIP call, so it runs without a GPU
-    assert L.emb_kv_append(None, None, 0, 1, None, None, 16, None, None, 1, 128, None) == -1
+    assert L.emb_kv_append(None, None, 0, 1, None, None, 16, None, None, None, 1, 128, None) == -1
     assert "null" in emb.last_error()
     buf = C.c_void_p(256)  # aligned, never dereferenced: rejected on shape first
-    assert L.emb_kv_append(buf, buf, 100, 4, buf, None, 16, buf, buf, 1, 100, None) == -1
+    assert L.emb_kv_append(buf, buf, 100, 4, buf, None, 16, buf, buf, None, 1, 100, None) == -1
     assert "multiple of 8" in emb.last_error()
+    assert L.emb_kv_append(buf, buf, 128, 4, buf, None, 16, buf, buf, C.c_void_p(264), 1, 128, None) == -1
+    assert "aligned" in emb.last_error()
+    # W8: shapes outside the Marlin contract are refused before any launch
+    assert L.emb_w8a16_gemm(buf, 0, 96, buf, buf, 4, 96, 96, buf, 96, 0, None) == -4
+    assert "out_features" in emb.last_error()
+    assert L.cosmos3_w8a16_linear_f32(buf, buf, buf, buf, 4, 128, 128, 9, 512, 1, 128, None) == -1
+    assert L.emb_w8a16_gemm(buf, 0, 128, buf, buf, 4, 128, 128, buf, 128, 7, None) == -1
     assert L.emb_kv_gather(buf, buf, buf, 0, None, 16, buf, buf, 1, 128, None) == -1
     assert L.lingbot_runtime_kv_update_f32(buf, buf, buf, buf, buf, 4, 1, 64, 4, None) == -1
     assert "capacity" in emb.last_error()
