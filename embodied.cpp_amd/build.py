@@ -26,19 +26,22 @@ ARCH = "gfx950"
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", f"-I{ROOT / 'include'}", f"-I{CSRC}", "-Wall",
           "-Wno-unused-function"]
-# -amdgpu-mfma-vgpr-form: MFMA accumulators stay in arch VGPRs.  Left to its
-# heuristic the compiler keeps the attention accumulators in AGPRs and, because
-# the (rarely taken) online-softmax rescale multiplies them with VALU ops,
-# copies all of them AGPR -> VGPR at the top of every key tile.
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-          "-munsafe-fp-atomics", "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+          "-munsafe-fp-atomics"]
+# Per-file extras.  -amdgpu-mfma-vgpr-form: MFMA accumulators stay in arch
+# VGPRs.  Left to its heuristic the compiler keeps the attention accumulators in
+# AGPRs and, because the (rarely taken) online-softmax rescale multiplies them
+# with VALU ops, copies all of them AGPR -> VGPR at the top of every key tile.
+# The GEMM must not get it: its 128 accumulators plus staging registers only fit
+# in the arch + accumulation file together (with it, the QKV epilogue spills).
+EXTRA = {"paged_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _compile(src: Path, asm: bool) -> Path:
     obj = BUILD / (src.name + ".o")
     cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
     if src.suffix == ".hip":
-        cmd[1:1] = DEVICE
+        cmd[1:1] = DEVICE + EXTRA.get(src.name, [])
         cmd.insert(1, "-xhip")
     if asm and src.suffix == ".hip":
         cmd += ["-save-temps=obj"]

@@ -191,62 +191,124 @@ __device__ __forceinline__ void page_rsrc(const KParams &p, const uint16_t *vbas
 #pragma unroll
     for (int pg = 0; pg < Geo<D>::PAGES; ++pg) {
         const int32_t page = pid[pg];
-        const int32_t rows = page < 0 ? 0 : min(max(lim - (k0 + pg * 16), 0), 16);
+        // readfirstlane: the clamp may be selected as a VALU op, and a
+        // descriptor word in a VGPR turns every load into a waterfall loop
+        const int32_t rows =
+            __builtin_amdgcn_readfirstlane(page < 0 ? 0 : min(max(lim - (k0 + pg * 16), 0), 16));
         const int64_t off = page < 0 ? 0 : ((int64_t)page * p.hkv + kvh) * (16 * D);
         kr[pg] = __builtin_amdgcn_make_buffer_rsrc((void *)(p.k_pool + off), 0, rows * D * 2, RSRC_W3);
         vr[pg] = __builtin_amdgcn_make_buffer_rsrc((void *)(vbase + off), 0, rows > 0 ? 16 * D * 2 : 0, RSRC_W3);
     }
 }
 
+// Raw buffer descriptor over [base, base + bytes) (stride 0, 32-bit records),
+// its words forced into SGPRs (the arguments are wave-uniform).
+__device__ __forceinline__ u32x4 buf_desc(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
+                 (uint32_t)__builtin_amdgcn_readfirstlane(bytes), RSRC_W3};
+}
+
+// vmcnt(N) with the other counters left alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+
+// One global -> LDS copy of 16 bytes a lane: lane i's 16 bytes at byte offset
+// voff of the buffer land at LDS byte m0 + 16 i (bytes past the buffer's end
+// land as zeros).  Written as inline asm on purpose: the compiler cannot tell
+// the pipeline stages apart, so for its own form of this load it waits for
+// every outstanding copy (vmcnt(0)) before the next LDS read of any stage --
+// the prefetch included.  The kernel counts these loads itself (wait_vmcnt).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const u32x4 &desc, uint32_t m0, uint32_t voff) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"  // SALU write of M0 -> LDS-DMA read of M0: one wait state
+        "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0),
+        "v"(voff), "s"(desc)
+        : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // DMA path: the tile's K rows and f16 V-shadow pages go straight into the
-// stage.  Wave w issues 1 KB blocks b = 4j + w of each image; block b of the
+// stage.  Wave w copies 1 KB blocks b = 4j + w of each image; block b of the
 // K image holds key rows [b*64/CH, (b+1)*64/CH), so lane i loads the global
 // chunk that the XOR swizzle puts at slot (b*64 + i) % CH of its row.  A block
-// never crosses a page, so one resource serves all 64 lanes.
+// never crosses a page, so one descriptor serves all 64 lanes.  The per-lane
+// byte offsets do not depend on the tile and are computed once.
 template <int D>
-__device__ __forceinline__ void issue_dma(const KParams &p, const int32_t *pt, int32_t k0, int32_t lim, int32_t kvh,
-                                          uint16_t *stage) {
+struct DmaPlan {
     using G = Geo<D>;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    int32_t pid[G::PAGES];
-    tile_pages<D>(pt, pid);
-    __amdgpu_buffer_rsrc_t kr[G::PAGES], vr[G::PAGES];
-    page_rsrc<D>(p, p.v16_pool, pid, k0, lim, kvh, kr, vr);
-    constexpr int RB = 64 / G::CH;  // key rows per K block
+    static constexpr int NB = G::BLOCKS / 4;  // blocks per wave and image
+    static constexpr int PER_TILE = 2 * NB;   // copies per wave and tile
+    static constexpr int RB = 64 / G::CH;     // key rows per K block
+    uint32_t koff[NB], voff[NB];
+    int wave;
+
+    __device__ __forceinline__ void init() {
+        const int lane = threadIdx.x & 63;
+        wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
-    for (int j = 0; j < G::BLOCKS / 4; ++j) {
-        const int b = j * 4 + wave;
-        const int q = b * 64 + lane;
-        const int r = q / G::CH, s = q % G::CH;
-        const int c = s ^ (r & G::SWZ);
-        __amdgpu_buffer_rsrc_t rk;
-        // page of block b = (4j + w) * RB / 16: j*RB/4 for RB <= 4 (w < 4),
-        // 2j + w/2 for RB = 8 (D = 64)
-        if constexpr (RB <= 4)
-            rk = kr[(j * RB) / 4];
-        else
-            rk = (wave >> 1) ? kr[2 * j + 1] : kr[2 * j];
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(stage + b * 512), 16, ((r & 15) * D + c * 8) * 2,
-                                                 0, 0, 0);
-    }
-    // V image: page pp covers blocks [pp*D/32, (pp+1)*D/32)
-#pragma unroll
-    for (int j = 0; j < G::BLOCKS / 4; ++j) {
-        const int b = j * 4 + wave;
-        __amdgpu_buffer_rsrc_t rv;
-        int pp_lo;
-        if constexpr (D >= 128) {
-            pp_lo = (j * 4 * 32) / D;
-            rv = vr[pp_lo];
-        } else {
-            pp_lo = 2 * j + (wave >> 1);
-            rv = (wave >> 1) ? vr[2 * j + 1] : vr[2 * j];
+        for (int j = 0; j < NB; ++j) {
+            const int b = j * 4 + wave;
+            const int q = b * 64 + lane;
+            const int r = q / G::CH, sl = q % G::CH;
+            const int c = sl ^ (r & G::SWZ);
+            koff[j] = ((r & 15) * D + c * 8) * 2;
+            // V image: page pp covers blocks [pp*D/32, (pp+1)*D/32)
+            const int pp = D >= 128 ? (j * 4 * 32) / D : 2 * j + (wave >> 1);
+            voff[j] = b * 1024 - pp * D * 32 + lane * 16;
         }
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void *)(stage + G::K_ELEMS + b * 512), 16,
-                                                 b * 1024 - pp_lo * D * 32 + lane * 16, 0, 0, 0);
     }
-}
+
+    // Copies tile keys [k0, k0 + KT) into the stage at LDS byte address st:
+    // K rows below lim = min(n_keys, capacity), V pages of mapped pages.
+    __device__ __forceinline__ void issue(const KParams &p, const int32_t *pt, int32_t k0, int32_t lim, int32_t kvh,
+                                          uint32_t st) const {
+        int32_t pid[G::PAGES];
+        tile_pages<D>(pt, pid);
+        u32x4 kd[G::PAGES], vd[G::PAGES];
+#pragma unroll
+        for (int pg = 0; pg < G::PAGES; ++pg) {
+            const int32_t page = pid[pg];
+            const int32_t rows = page < 0 ? 0 : min(max(lim - (k0 + pg * 16), 0), 16);
+            const int64_t off = page < 0 ? 0 : ((int64_t)page * p.hkv + kvh) * (16 * D);
+            kd[pg] = buf_desc(p.k_pool + off, rows * D * 2);
+            vd[pg] = buf_desc(p.v16_pool + off, rows > 0 ? 16 * D * 2 : 0);
+        }
+        // The descriptors may come from VALU writes of SGPRs (readfirstlane);
+        // a VMEM read of such an SGPR needs 5 wait states, which the compiler
+        // does not insert for inline-asm operands.
+        asm volatile("s_nop 4");
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int b = j * 4 + wave;
+            u32x4 dk;
+            // page of K block b = (4j + w) * RB / 16: j*RB/4 for RB <= 4 (w < 4),
+            // 2j + w/2 for RB = 8 (D = 64)
+            if constexpr (RB <= 4)
+                dk = kd[(j * RB) / 4];
+            else
+                dk = (wave >> 1) ? kd[2 * j + 1] : kd[2 * j];
+            lds_copy16(dk, __builtin_amdgcn_readfirstlane(st + b * 1024), koff[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int b = j * 4 + wave;
+            u32x4 dv;
+            if constexpr (D >= 128)
+                dv = vd[(j * 4 * 32) / D];
+            else
+                dv = (wave >> 1) ? vd[2 * j + 1] : vd[2 * j];
+            lds_copy16(dv, __builtin_amdgcn_readfirstlane(st + G::K_ELEMS * 2 + b * 1024), voff[j]);
+        }
+    }
+};
 
 // Register paths: global -> registers (in flight during the compute of the
 // previous tile) -> converted and written into the stage image.
@@ -399,7 +461,10 @@ template <int D, int MASK, int LD, bool QF32>
 __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams p) {
     using G = Geo<D>;
     constexpr bool VALID = LD == LD_VALID;
-    __shared__ __attribute__((aligned(16))) uint16_t smem[3 * G::STAGE];
+    // four stages when the copies bypass registers (a tile's loads get two
+    // iterations to land), three otherwise
+    constexpr int NST = LD == LD_DMA ? 4 : 3;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[NST * G::STAGE];
     __shared__ __attribute__((aligned(16))) int32_t pt[VALID ? 4 : SEG_PAGES];
 
     // XCD-aware order: hardware ids go round-robin over the 8 XCDs, so logical
@@ -439,7 +504,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     // Query fragment: B operand of S^T = K Q^T.  Lane l holds row l%32,
     // dims kk*16 + (l/32)*8 + [0, 8).
     bf16x8 qf[D / 16];
-    {
+    auto load_q = [&]() {
         const int64_t qoff = (int64_t)(q_begin + tok) * p.q_stride + (int64_t)head * D + lhi * 8;
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
@@ -463,7 +528,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             if (D >= 256) asm volatile("" : "+a"(w));
             qf[kk] = __builtin_bit_cast(bf16x8, w);
         }
-    }
+    };
 
     // Key range of this workgroup: mask bounds, then this split's share.
     const int32_t last_row = min(row0 + ROWS_PER_WG, rows) - 1;
@@ -497,13 +562,16 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     const int32_t p_end = (min(lim, t_hi * G::KT) + 15) / 16;
     int32_t seg_p0 = t_lo * G::PAGES;
 
-    // Starts the transfer of tile tt into stage st (a uniform call: every
+    // Starts the transfer of tile tt into stage si (a uniform call: every
     // thread of the workgroup reaches it).  DMA writes the stage directly;
-    // the register paths fill l, which finish() writes out.  The direct paths
+    // the register paths fill l, which l.store() writes out.  The direct paths
     // read page ids from the LDS copy of the block table, reloading the next
     // segment when tt leaves it (every wave is past its last read of the old
     // one: the previous tile ended with a barrier).
-    auto issue = [&](RegLoader<D, VALID> &l, int32_t tt, uint16_t *st) {
+    DmaPlan<D> dma;
+    if constexpr (LD == LD_DMA) dma.init();
+    const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
+    auto issue = [&](RegLoader<D, VALID> &l, int32_t tt, int si) {
         if constexpr (LD == LD_VALID) {
             l.issue_valid(p, valid_b, bt_b, tt * G::KT, nk, kvh);
         } else {
@@ -515,16 +583,10 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                 pi = 0;
             }
             if constexpr (LD == LD_DMA)
-                issue_dma<D>(p, pt + pi, tt * G::KT, lim, kvh, st);
+                dma.issue(p, pt + pi, tt * G::KT, lim, kvh, smem_lds + si * (G::STAGE * 2));
             else
                 l.issue_direct(p, pt + pi, tt * G::KT, lim, kvh);
         }
-    };
-    auto finish = [&](const RegLoader<D, VALID> &l, uint16_t *st) {
-        if constexpr (LD == LD_DMA)
-            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this thread's LDS-bound loads landed
-        else
-            l.store(st);
     };
 
     // S^T = K Q^T of the tile in stage st: in block kb, lane holds keys
@@ -541,38 +603,51 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
         }
     };
 
-    // Prologue: tiles t_lo and t_lo+1 staged, S of tile t_lo computed.
+    // Prologue: the first NST-1 tiles staged, S of tile t_lo computed.
     RegLoader<D, VALID> ld;
-    if (t_lo < t_hi) {
-        if (LD != LD_VALID) {
+    if constexpr (LD == LD_DMA) {
+        if (t_lo < t_hi) {
             load_segment(bt_b, seg_p0, p_end, pt);
             __syncthreads();
+            issue(ld, t_lo, 0);
+            if (t_lo + 1 < t_hi) issue(ld, t_lo + 1, 1);
+            if (t_lo + 2 < t_hi) issue(ld, t_lo + 2, 2);
         }
-        RegLoader<D, VALID> l1;
-        issue(ld, t_lo, smem);
-        if (t_lo + 1 < t_hi) issue(l1, t_lo + 1, smem + G::STAGE);
-        finish(ld, smem);
-        if (t_lo + 1 < t_hi) finish(l1, smem + G::STAGE);
-        __syncthreads();
+        load_q();  // its latency overlaps the copies'
+    } else {
+        load_q();
+        if (t_lo < t_hi) {
+            if (LD != LD_VALID) {
+                load_segment(bt_b, seg_p0, p_end, pt);
+                __syncthreads();
+            }
+            RegLoader<D, VALID> l1;
+            issue(ld, t_lo, 0);
+            if (t_lo + 1 < t_hi) issue(l1, t_lo + 1, 1);
+            ld.store(smem);
+            if (t_lo + 1 < t_hi) l1.store(smem + G::STAGE);
+        }
     }
     // Every load issued so far (the query fragment included) has landed.
     // Without this the compiler, merging the path that skips the prologue,
     // treats the query registers as possibly in flight inside the loop and
     // waits for all outstanding loads -- the prefetch included -- before the
     // first MFMA of every tile.
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    wait_vmcnt<0>();
+    __syncthreads();
     f32x16 s_cur[G::KB];
     qk(smem, s_cur);
 
-    // Stage `cur` holds tile t, nx1 tile t+1, nx2 receives tile t+2.  Past the
-    // end, the extra S and the stores work on stale stage contents that
-    // nothing reads.
+    // Stage `cur` holds tile t, nx1 tile t+1, and the last stage receives
+    // tile t + NST - 1.  Past the end, the extra S and the stores work on
+    // stale stage contents that nothing reads.
     int cur = 0;
     for (int32_t t = t_lo; t < t_hi; ++t) {
         const int32_t k0 = t * G::KT;
-        const int nx1 = cur == 2 ? 0 : cur + 1;
-        const int nx2 = nx1 == 2 ? 0 : nx1 + 1;
-        if (t + 2 < t_hi) issue(ld, t + 2, smem + nx2 * G::STAGE);
+        const int nx1 = cur + 1 == NST ? 0 : cur + 1;
+        const int nxl = cur == 0 ? NST - 1 : cur - 1;  // receives tile t + NST - 1
+        const bool more = t + NST - 1 < t_hi;
+        if (more) issue(ld, t + NST - 1, nxl);
 
         // mask (raw score units) and row max of tile t
         bool tile_full = k0 + G::KT <= nk;
@@ -638,7 +713,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             }
 
         // O^T += V^T P^T of tile t (MFMA, one 16-key page a step) alongside the
-        // staging of tile t+2
+        // staging of the next tiles
         const uint16_t *st = smem + cur * G::STAGE;
 #pragma unroll
         for (int kb = 0; kb < G::KB; ++kb)
@@ -650,7 +725,15 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                     acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vw), pf[kb][pg],
                                                                       acc_o[dt], 0, 0, 0);
                 }
-        finish(ld, smem + nx2 * G::STAGE);
+        if constexpr (LD == LD_DMA) {
+            // tile t+2 (needed by the next S) has landed; tile t+3 may still fly
+            if (more)
+                wait_vmcnt<DmaPlan<D>::PER_TILE>();
+            else
+                wait_vmcnt<0>();
+        } else if (more) {
+            ld.store(smem + nxl * G::STAGE);
+        }
         __syncthreads();
 #pragma unroll
         for (int kb = 0; kb < G::KB; ++kb) s_cur[kb] = s_nxt[kb];

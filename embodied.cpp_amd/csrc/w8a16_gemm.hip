@@ -41,6 +41,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <type_traits>
 
 #include "emb_common.h"
 
@@ -50,6 +51,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 256, BN = 128, BK = 64;
 constexpr int AS = BK + 8;  // bf16 elements per staged x row (bank spread)
@@ -262,6 +264,109 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
 
     // Epilogue: lane holds column n = n0 + wn*64 + j*32 + lrow and rows
     // m0 + wm*128 + i*32 + (r/4)*8 + lhi*4 + r%4.
+    if constexpr (MODE == Y_QKV) {
+        // Row table in the (now free) A tile: for each of the tile's BM rows the
+        // element offset of its page (page * hkv * 16 * head_dim) with the
+        // in-page token in the low 4 bits, or -1 when the row is past M or its
+        // slot is out of range or unmapped.  A page offset is a multiple of 16
+        // elements, so its low 4 bits are free.
+        int64_t *rowtab = reinterpret_cast<int64_t *>(as);
+        __syncthreads();  // every wave is past its last fragment read of as
+        for (int r = threadIdx.x; r < BM; r += 256) {
+            const int32_t m = m0 + r;
+            int64_t e = -1;
+            if (m < p.M) {
+                const int32_t slot = p.slots[m];
+                if (slot >= 0 && slot < p.capacity) {
+                    const int32_t page = p.bt ? p.bt[slot >> 4] : (slot >> 4);
+                    if (page >= 0) e = (int64_t)page * p.hkv * 16 * p.head_dim + (slot & 15);
+                }
+            }
+            rowtab[r] = e;
+        }
+        __syncthreads();
+        const int64_t hstride = 16 * (int64_t)p.head_dim;
+        // one column block at a time with a compile-time j: the unroller gives
+        // up on a two-trip loop around this body, and a runtime j would index
+        // the accumulators through scratch memory
+        auto store_cols = [&](auto jc) __attribute__((always_inline)) {
+            constexpr int j = decltype(jc)::value;
+            const int32_t n = n0 + wn * 64 + j * 32 + lrow;
+            if (n >= p.N) return;
+            const float s = __builtin_bit_cast(float, (uint32_t)p.scales[(n >> 5) * 32 + ((n & 31) >> 3) * 2 +
+                                                                        ((n & 7) >> 1) * 8 + (n & 1)]
+                                                             << 16);
+            if (n < p.n_q) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int32_t m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                        if (m < p.M)
+                            reinterpret_cast<uint16_t *>(p.y)[(int64_t)m * p.ldy + n] =
+                                (uint16_t)f32_to_bf16_bits(acc[i][j][r] * s);
+                    }
+                return;
+            }
+            const int32_t c = n - p.n_q;
+            const bool is_v = c >= p.n_kv;
+            const int32_t cc = is_v ? c - p.n_kv : c;
+            const int32_t d = cc % p.head_dim;
+            const int64_t hoff = (cc / p.head_dim) * hstride;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int rl = wm * 128 + i * 32 + g * 8 + lhi * 4;  // four consecutive rows
+                    int64_t e[4];
+                    uint32_t b[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        e[k] = rowtab[rl + k];
+                        b[k] = f32_to_bf16_bits(acc[i][j][g * 4 + k] * s);
+                    }
+                    if (!is_v) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (e[k] >= 0) p.k_pool[(e[k] & ~15LL) + hoff + (e[k] & 15) * p.head_dim + d] = b[k];
+                        continue;
+                    }
+                    // V: four rows on consecutive slots of one page starting at a
+                    // multiple of 4 are contiguous in the [d][16] page rows (and in
+                    // the shadow's order, which keeps bits 0-1 of the token)
+                    const bool run = e[0] >= 0 && (e[0] & 3) == 0 && e[1] == e[0] + 1 && e[2] == e[0] + 2 &&
+                                     e[3] == e[0] + 3;
+                    if (run) {
+                        const int64_t pb = (e[0] & ~15LL) + hoff;
+                        const int t0 = (int)(e[0] & 15);
+                        *reinterpret_cast<u32x2 *>(p.v_pool + pb + d * 16 + t0) =
+                            u32x2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
+                        if (p.v16_pool) {
+                            uint32_t h16[4];
+#pragma unroll
+                            for (int k = 0; k < 4; ++k)
+                                h16[k] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_bit_cast(float, b[k] << 16));
+                            *reinterpret_cast<u32x2 *>(p.v16_pool + pb + emb::v16_index(d, t0)) =
+                                u32x2{h16[0] | (h16[1] << 16), h16[2] | (h16[3] << 16)};
+                        }
+                        continue;
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        if (e[k] < 0) continue;
+                        const int64_t pb = (e[k] & ~15LL) + hoff;
+                        const int t = (int)(e[k] & 15);
+                        p.v_pool[pb + d * 16 + t] = (uint16_t)b[k];
+                        if (p.v16_pool)
+                            p.v16_pool[pb + emb::v16_index(d, t)] =
+                                __builtin_bit_cast(uint16_t, (_Float16)__builtin_bit_cast(float, b[k] << 16));
+                    }
+                }
+        };
+        store_cols(std::integral_constant<int, 0>{});
+        store_cols(std::integral_constant<int, 1>{});
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int32_t n = n0 + wn * 64 + j * 32 + lrow;
@@ -280,33 +385,10 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
                     reinterpret_cast<float *>(p.y)[(int64_t)m * p.ldy + n] = v;
                 } else {
                     const uint32_t bits = f32_to_bf16_bits(v);
-                    if (MODE == Y_BF16) {
+                    if (MODE == Y_BF16)
                         reinterpret_cast<uint16_t *>(p.y)[(int64_t)m * p.ldy + n] = (uint16_t)bits;
-                    } else if (MODE == Y_F32_ROUNDED) {
+                    else
                         reinterpret_cast<float *>(p.y)[(int64_t)m * p.ldy + n] = __builtin_bit_cast(float, bits << 16);
-                    } else {  // Y_QKV
-                        if (n < p.n_q) {
-                            reinterpret_cast<uint16_t *>(p.y)[(int64_t)m * p.ldy + n] = (uint16_t)bits;
-                        } else {
-                            const int32_t slot = p.slots[m];
-                            if (slot < 0 || slot >= p.capacity) continue;
-                            const int32_t page = p.bt ? p.bt[slot >> 4] : (slot >> 4);
-                            if (page < 0) continue;
-                            const int32_t c = n - p.n_q;
-                            const bool is_v = c >= p.n_kv;
-                            const int32_t cc = is_v ? c - p.n_kv : c;
-                            const int32_t h = cc / p.head_dim, d = cc % p.head_dim;
-                            const int64_t pbase = ((int64_t)page * p.hkv + h) * 16 * p.head_dim;
-                            if (!is_v) {
-                                p.k_pool[pbase + (slot & 15) * p.head_dim + d] = (uint16_t)bits;
-                            } else {
-                                p.v_pool[pbase + d * 16 + (slot & 15)] = (uint16_t)bits;
-                                if (p.v16_pool)
-                                    p.v16_pool[pbase + emb::v16_index(d, slot & 15)] = __builtin_bit_cast(
-                                        uint16_t, (_Float16)__builtin_bit_cast(float, bits << 16));
-                            }
-                        }
-                    }
                 }
             }
     }
@@ -399,6 +481,7 @@ int emb_w8a16_qkv_append(const void *x, int32_t x_is_f32, int64_t ldx, const int
     EMB_CHECK_ARG(slots && k_pool && v_pool, "null slots/pool");
     EMB_CHECK_ARG(n_q >= 0 && n_kv_heads > 0 && head_dim > 0 && capacity > 0, "bad sizes");
     EMB_CHECK_ARG(n_q == 0 || (q_out && ldq >= n_q), "q_out and ldq >= n_q required when n_q > 0");
+    EMB_CHECK_ARG(aligned16(v_pool) && aligned16(v16_pool), "v_pool and v16_pool must be 16-byte aligned");
     GParams p{};
     p.x = x;
     p.ldx = ldx;
