@@ -66,6 +66,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -79,7 +80,11 @@ constexpr int ROWS_PER_WAVE = 32;
 constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
 constexpr float RESCALE_TH = 8.0f;  // log2 units
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr int SEG_PAGES = 1024;  // block-table entries held in LDS at a time (16384 keys)
+constexpr int SEG_PAGES = 1024;
+// LDS fragment reads kept in flight ahead of the MFMA that consumes them: the
+// LDS latency is several MFMA issue slots, and the compiler's own schedule
+// issues each read just one MFMA ahead.
+constexpr int AHEAD = 4;  // block-table entries held in LDS at a time (16384 keys)
 constexpr uint32_t RSRC_W3 = 0x00020000u;  // buffer resource word 3 (raw, 32-bit elements)
 
 enum { LD_DMA = 0, LD_REG = 1, LD_VALID = 2 };
@@ -137,6 +142,16 @@ struct KParams {
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+
+// Lane l and lane l ^ 32 of x, as a pair, by one VALU lane swap: the first
+// element is x of lane l & 31, the second x of lane l | 32 (so their max or
+// sum is the same in both halves of the wave).
+__device__ __forceinline__ void half_pair(float x, float &a, float &b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    a = __builtin_bit_cast(float, (uint32_t)r[0]);
+    b = __builtin_bit_cast(float, (uint32_t)r[1]);
+}
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     uint32_t u = __builtin_bit_cast(uint32_t, f);
@@ -494,6 +509,8 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     const int lhi = lane >> 5;
     const int32_t my_row = row0 + wave * ROWS_PER_WAVE + lrow;
     const bool row_ok = my_row < rows;
+    // a wave past the last row only helps stage tiles (and meets the barriers)
+    const bool wave_live = __builtin_amdgcn_readfirstlane(row0 + wave * ROWS_PER_WAVE) < rows;
     const int32_t tok = row_ok ? my_row / p.G : 0;
     const int32_t head = kvh * p.G + (row_ok ? my_row % p.G : 0);
     const int32_t qpos = qpos0 + tok;
@@ -522,11 +539,20 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                     w = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(p.q) + qoff + kk * 16);
                 }
             }
-            // At D = 256 the accumulators (128) and the rest of the loop fill the
-            // 256 arch VGPRs; the read-only query fragment lives in AGPRs, which
-            // MFMA reads directly.
-            if (D >= 256) asm volatile("" : "+a"(w));
             qf[kk] = __builtin_bit_cast(bf16x8, w);
+        }
+    };
+    // At D = 256 the accumulators (128) and the rest of the loop fill the 256
+    // arch VGPRs; the read-only query fragment moves to AGPRs, which MFMA reads
+    // directly.  (Done once the loads have landed, so the move does not wait.)
+    auto pin_q = [&]() {
+        if constexpr (D >= 256) {
+#pragma unroll
+            for (int kk = 0; kk < D / 16; ++kk) {
+                u32x4 w = __builtin_bit_cast(u32x4, qf[kk]);
+                asm volatile("" : "+a"(w));
+                qf[kk] = __builtin_bit_cast(bf16x8, w);
+            }
         }
     };
 
@@ -606,6 +632,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     // Prologue: the first NST-1 tiles staged, S of tile t_lo computed.
     RegLoader<D, VALID> ld;
     if constexpr (LD == LD_DMA) {
+        load_q();  // in flight with the block-table fetch and the copies
         if (t_lo < t_hi) {
             load_segment(bt_b, seg_p0, p_end, pt);
             __syncthreads();
@@ -613,7 +640,6 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             if (t_lo + 1 < t_hi) issue(ld, t_lo + 1, 1);
             if (t_lo + 2 < t_hi) issue(ld, t_lo + 2, 2);
         }
-        load_q();  // its latency overlaps the copies'
     } else {
         load_q();
         if (t_lo < t_hi) {
@@ -634,9 +660,10 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     // waits for all outstanding loads -- the prefetch included -- before the
     // first MFMA of every tile.
     wait_vmcnt<0>();
+    pin_q();
     __syncthreads();
     f32x16 s_cur[G::KB];
-    qk(smem, s_cur);
+    if (wave_live) qk(smem, s_cur);
 
     // Stage `cur` holds tile t, nx1 tile t+1, and the last stage receives
     // tile t + NST - 1.  Past the end, the extra S and the stores work on
@@ -649,82 +676,118 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
         const bool more = t + NST - 1 < t_hi;
         if (more) issue(ld, t + NST - 1, nxl);
 
-        // mask (raw score units) and row max of tile t
-        bool tile_full = k0 + G::KT <= nk;
-        if (MASK == EMB_MASK_CHUNK) tile_full = tile_full && k0 >= full_lo && k0 + G::KT <= full_hi;
-        if (MASK == EMB_MASK_TOKEN || MASK == EMB_MASK_ADD || MASK == EMB_MASK_BLOCKMAP) tile_full = false;
-        if (!tile_full) {  // one uniform branch around the whole per-key mask
+        if (wave_live) {
+            // mask (raw score units) and row max of tile t
+            bool tile_full = k0 + G::KT <= nk;
+            if (MASK == EMB_MASK_CHUNK) tile_full = tile_full && k0 >= full_lo && k0 + G::KT <= full_hi;
+            if (MASK == EMB_MASK_TOKEN || MASK == EMB_MASK_ADD || MASK == EMB_MASK_BLOCKMAP) tile_full = false;
+            if (!tile_full) {  // one uniform branch around the whole per-key mask
 #pragma unroll
-            for (int kb = 0; kb < G::KB; ++kb) {
+                for (int kb = 0; kb < G::KB; ++kb) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float x = s_cur[kb][r];
-                    const int32_t j = k0 + kb * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-                    bool vis = row_ok && j < nk;
-                    if (MASK == EMB_MASK_CHUNK) {
-                        const int32_t qc = qpos / p.chunk, kc = j / p.chunk;
-                        vis = vis && kc <= qc && (p.window < 0 || qc - kc <= p.window);
-                    } else if (MASK == EMB_MASK_TOKEN) {
-                        vis = vis && reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
-                                                                              (int64_t)tok * p.mask_q_stride + j] != 0;
-                    } else if (MASK == EMB_MASK_ADD) {
-                        if (vis)
-                            x += p.inv_scale * reinterpret_cast<const float *>(p.mask)[(int64_t)b * p.mask_b_stride +
-                                                                                      (int64_t)tok * p.mask_q_stride + j];
-                    } else if (MASK == EMB_MASK_BLOCKMAP) {
-                        vis = vis && p.bmap[(int64_t)b * p.bmap_b_stride + (int64_t)(tok / p.bsize) * p.bmap_cols +
-                                            j / p.bsize] != 0;
-                        if (vis && p.mask)
-                            vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
-                                                                            (int64_t)tok * p.mask_q_stride + j] != 0;
+                    for (int r = 0; r < 16; ++r) {
+                        float x = s_cur[kb][r];
+                        const int32_t j = k0 + kb * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                        bool vis = row_ok && j < nk;
+                        if (MASK == EMB_MASK_CHUNK) {
+                            const int32_t qc = qpos / p.chunk, kc = j / p.chunk;
+                            vis = vis && kc <= qc && (p.window < 0 || qc - kc <= p.window);
+                        } else if (MASK == EMB_MASK_TOKEN) {
+                            vis = vis && reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                                  (int64_t)tok * p.mask_q_stride + j] != 0;
+                        } else if (MASK == EMB_MASK_ADD) {
+                            if (vis)
+                                x += p.inv_scale * reinterpret_cast<const float *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                                          (int64_t)tok * p.mask_q_stride + j];
+                        } else if (MASK == EMB_MASK_BLOCKMAP) {
+                            vis = vis && p.bmap[(int64_t)b * p.bmap_b_stride + (int64_t)(tok / p.bsize) * p.bmap_cols +
+                                                j / p.bsize] != 0;
+                            if (vis && p.mask)
+                                vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                                (int64_t)tok * p.mask_q_stride + j] != 0;
+                        }
+                        s_cur[kb][r] = vis ? x : -INFINITY;
                     }
-                    s_cur[kb][r] = vis ? x : -INFINITY;
                 }
             }
-        }
-        float mt = -INFINITY;
+            float mt = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < G::KB; ++kb)
+            for (int kb = 0; kb < G::KB; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s_cur[kb][r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        // wave-uniform lazy rescale
-        if (__builtin_amdgcn_ballot_w64(mt > m_run + p.th_raw) != 0) {
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
+                for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s_cur[kb][r]);
+            {
+                float a, c;
+                half_pair(mt, a, c);
+                mt = fmaxf(a, c);
+            }
+            // wave-uniform lazy rescale
+            if (__builtin_amdgcn_ballot_w64(mt > m_run + p.th_raw) != 0) {
+                const float m_new = fmaxf(m_run, mt);
+                const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
 #pragma unroll
-            for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
-            l_run *= alpha;
-            m_run = m_new;
-        }
-
-        // S of tile t+1 (MFMA) alongside P of tile t (VALU)
-        f32x16 s_nxt[G::KB];
-        qk(smem + nx1 * G::STAGE, s_nxt);
-        const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * p.c_log2;
-        f16x8 pf[G::KB][2];
-#pragma unroll
-        for (int kb = 0; kb < G::KB; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[kb][r], p.c_log2, neg_mc));
-                l_run += e;
-                pf[kb][r >> 3][r & 7] = (_Float16)e;
+                for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
+                l_run *= alpha;
+                m_run = m_new;
             }
 
-        // O^T += V^T P^T of tile t (MFMA, one 16-key page a step) alongside the
-        // staging of the next tiles
-        const uint16_t *st = smem + cur * G::STAGE;
+            // S of tile t+1 (MFMA) alongside P of tile t (VALU), then
+            // O^T += V^T P^T of tile t (MFMA, one 16-key page a step).  The
+            // order is fixed step by step (sched_barrier): each step issues one
+            // MFMA, the LDS read AHEAD steps later, and (S phase) 256/D softmax
+            // elements, whose VALU work runs while the MFMA executes.
+            constexpr int KS = D / 16;              // k-steps of one 32-key S block
+            constexpr int NS = G::KB * KS;          // S MFMAs a tile
+            constexpr int NPV = G::KB * 2 * (D / 32);  // P.V MFMAs a tile
+            constexpr int EPM = G::KB * 16 / NS;    // softmax elements per S step
+            const uint16_t *stk = smem + nx1 * G::STAGE;
+            const uint16_t *stv = smem + cur * G::STAGE;
+            auto read_k = [&](int i) {
+                return *reinterpret_cast<const u32x4 *>(&stk[k_off<D>((i / KS) * 32 + lrow, (i % KS) * 2 + lhi)]);
+            };
+            auto read_v = [&](int i) {  // i = (kb*2 + pg) * (D/32) + dt
+                return *reinterpret_cast<const u32x4 *>(
+                    &stv[v_off<D>(i / (D / 32), (i % (D / 32)) * 32 + lrow, lhi)]);
+            };
+            f32x16 s_nxt[G::KB];
+            const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * p.c_log2;
+            f16x8 pf[G::KB][2];
+            u32x4 kbuf[AHEAD];
 #pragma unroll
-        for (int kb = 0; kb < G::KB; ++kb)
+            for (int i = 0; i < AHEAD; ++i) kbuf[i] = read_k(i);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int pg = 0; pg < 2; ++pg)
+            for (int i = 0; i < NS; ++i) {
+                const int kb = i / KS, kk = i % KS;
+                s_nxt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kbuf[i % AHEAD]), qf[kk],
+                                                                   kk == 0 ? f32x16{} : s_nxt[kb], 0, 0, 0);
+                if (i + AHEAD < NS) kbuf[i % AHEAD] = read_k(i + AHEAD);
 #pragma unroll
-                for (int dt = 0; dt < D / 32; ++dt) {
-                    const u32x4 vw = *reinterpret_cast<const u32x4 *>(&st[v_off<D>(kb * 2 + pg, dt * 32 + lrow, lhi)]);
-                    acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vw), pf[kb][pg],
-                                                                      acc_o[dt], 0, 0, 0);
+                for (int u = 0; u < EPM; ++u) {
+                    const int el = i * EPM + u, eb = el / 16, r = el % 16;
+                    const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[eb][r], p.c_log2, neg_mc));
+                    pf[eb][r >> 3][r & 7] = (_Float16)e;
+                    // row sum of exactly the f16 weights the P.V product uses
+                    if (r & 1)
+                        l_run = __builtin_amdgcn_fdot2(f16x2{pf[eb][r >> 3][(r & 7) - 1], pf[eb][r >> 3][r & 7]},
+                                                       f16x2{(_Float16)1.0f, (_Float16)1.0f}, l_run, false);
                 }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            u32x4 vbuf[AHEAD];
+#pragma unroll
+            for (int i = 0; i < AHEAD; ++i) vbuf[i] = read_v(i);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < NPV; ++i) {
+                const int kp = i / (D / 32), dt = i % (D / 32);
+                acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vbuf[i % AHEAD]),
+                                                                  pf[kp >> 1][kp & 1], acc_o[dt], 0, 0, 0);
+                if (i + AHEAD < NPV) vbuf[i % AHEAD] = read_v(i + AHEAD);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int kb = 0; kb < G::KB; ++kb) s_cur[kb] = s_nxt[kb];
+        }  // wave_live
         if constexpr (LD == LD_DMA) {
             // tile t+2 (needed by the next S) has landed; tile t+3 may still fly
             if (more)
@@ -735,41 +798,94 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             ld.store(smem + nxl * G::STAGE);
         }
         __syncthreads();
-#pragma unroll
-        for (int kb = 0; kb < G::KB; ++kb) s_cur[kb] = s_nxt[kb];
         cur = nx1;
     }
-    l_run += __shfl_xor(l_run, 32);
-    if (!row_ok) return;
+    {
+        float a, c;
+        half_pair(l_run, a, c);
+        l_run = a + c;
+    }
 
-    if (p.splits > 1) {
-        const int64_t unit = (int64_t)(b * p.hkv + kvh) * p.splits + split;
-        const int64_t rowi = unit * ((int64_t)p.row_tiles * ROWS_PER_WG) + my_row;
-        float *wo = p.ws_o + rowi * D;
+    // Output rows: the normalised O (f32) or, with splits, the unnormalised
+    // partial with its (m, l).  Lane l holds dims dt*32 + j*8 + (l/32)*4 + [0,4)
+    // of row l%32, so a direct 16-byte store touches 64 rows (cache lines) per
+    // instruction.  Where the stages have room, each wave instead writes its 32
+    // rows x D block into LDS (16-byte chunk c of row r at chunk c ^ (r & 31),
+    // which spreads the 32 rows of one write over the banks) and stores whole
+    // rows: D*4 contiguous bytes per row, 1024/D rows an instruction.
+    const bool partial = p.splits > 1;
+    const int64_t unit_row0 =
+        partial ? ((int64_t)(b * p.hkv + kvh) * p.splits + split) * ((int64_t)p.row_tiles * ROWS_PER_WG) : 0;
+    if (partial && row_ok && lhi == 0) {
+        const int64_t rowi = unit_row0 + my_row;
+        p.ws_ml[rowi * 2] = m_run == -INFINITY ? -INFINITY : m_run * p.c_log2;
+        p.ws_ml[rowi * 2 + 1] = l_run;
+    }
+    const float sc = partial ? 1.0f : (l_run > 0.0f ? 1.0f / l_run : 0.0f);
+    constexpr int CHR = D / 4;  // 16-byte chunks in a row of D floats
+    if constexpr (NST * G::STAGE * 2 >= WAVES * ROWS_PER_WAVE * D * 4) {
+        // every wave is past its last stage read (the loop ended with a barrier)
+        float *ob = reinterpret_cast<float *>(smem) + wave * (ROWS_PER_WAVE * D);
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                f32x4 v = {acc_o[dt][j * 4], acc_o[dt][j * 4 + 1], acc_o[dt][j * 4 + 2], acc_o[dt][j * 4 + 3]};
-                *reinterpret_cast<f32x4 *>(wo + dt * 32 + j * 8 + lhi * 4) = v;
+                const int c = dt * 8 + j * 2 + lhi;
+                const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
+                                 acc_o[dt][j * 4 + 3] * sc};
+                *reinterpret_cast<f32x4 *>(ob + lrow * D + ((c ^ (lrow & (CHR - 1) & 31)) << 2)) = v;
             }
-        if (lhi == 0) {
-            p.ws_ml[rowi * 2] = m_run == -INFINITY ? -INFINITY : m_run * p.c_log2;
-            p.ws_ml[rowi * 2 + 1] = l_run;
+        constexpr int RPI = 64 / CHR;  // rows per store instruction
+        constexpr int NI = ROWS_PER_WAVE / RPI;
+        const int sub = lane / CHR, c = lane % CHR;
+        // all reads first (the accumulators are dead), then the stores back to back
+        f32x4 rv[NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int r = i * RPI + sub;
+            rv[i] = *reinterpret_cast<const f32x4 *>(ob + r * D + ((c ^ (r & (CHR - 1) & 31)) << 2));
         }
-        return;
+        __builtin_amdgcn_sched_barrier(0);
+        // lane r < 32 holds the destination (element offset) of row r of the
+        // wave, -1 past the last row; a store takes its rows' offsets by lane
+        // reads (scalar when one row fills the instruction)
+        float *const obase = partial ? p.ws_o : p.out;
+        int64_t dst_off = -1;
+        if (row_ok)
+            dst_off = partial ? (unit_row0 + my_row) * D
+                              : (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
+        const uint32_t off_lo = (uint32_t)dst_off, off_hi = (uint32_t)((uint64_t)dst_off >> 32);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            int64_t off;
+            if constexpr (RPI == 1) {
+                off = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(off_hi, i) << 32) |
+                                (uint32_t)__builtin_amdgcn_readlane(off_lo, i));
+            } else {
+                int64_t cand[RPI];
+#pragma unroll
+                for (int u = 0; u < RPI; ++u)
+                    cand[u] = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane(off_hi, i * RPI + u) << 32) |
+                                        (uint32_t)__builtin_amdgcn_readlane(off_lo, i * RPI + u));
+                off = cand[0];
+#pragma unroll
+                for (int u = 1; u < RPI; ++u) off = sub == u ? cand[u] : off;
+            }
+            if (off >= 0) *reinterpret_cast<f32x4 *>(obase + off + c * 4) = rv[i];
+        }
+    } else {
+        if (!row_ok) return;
+        float *dst = partial ? p.ws_o + (unit_row0 + my_row) * D
+                             : p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
+                                 acc_o[dt][j * 4 + 3] * sc};
+                *reinterpret_cast<f32x4 *>(dst + dt * 32 + j * 8 + lhi * 4) = v;
+            }
     }
-
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    float *op = p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
-#pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f32x4 v = {acc_o[dt][j * 4] * inv, acc_o[dt][j * 4 + 1] * inv, acc_o[dt][j * 4 + 2] * inv,
-                       acc_o[dt][j * 4 + 3] * inv};
-            *reinterpret_cast<f32x4 *>(op + dt * 32 + j * 8 + lhi * 4) = v;
-        }
 }
 
 // Combines split partials (m in log2 units): m = max m_s, l = sum l_s 2^(m_s - m),
