@@ -59,6 +59,7 @@
 
 #include <climits>
 #include <cmath>
+#include <type_traits>
 
 #include "emb_common.h"
 
@@ -281,47 +282,67 @@ struct DmaPlan {
         }
     }
 
-    // Copies tile keys [k0, k0 + KT) into the stage at LDS byte address st:
-    // K rows below lim = min(n_keys, capacity), V pages of mapped pages.
-    __device__ __forceinline__ void issue(const KParams &p, const int32_t *pt, int32_t k0, int32_t lim, int32_t kvh,
-                                          uint32_t st) const {
+    // Descriptors of one tile's pages: K covers the rows below lim =
+    // min(n_keys, capacity), V the whole page of a mapped page.
+    struct Descs {
+        u32x4 kd[G::PAGES], vd[G::PAGES];
+    };
+    __device__ __forceinline__ void prepare(const KParams &p, const int32_t *pt, int32_t k0, int32_t lim, int32_t kvh,
+                                            Descs &ds) const {
         int32_t pid[G::PAGES];
         tile_pages<D>(pt, pid);
-        u32x4 kd[G::PAGES], vd[G::PAGES];
 #pragma unroll
         for (int pg = 0; pg < G::PAGES; ++pg) {
             const int32_t page = pid[pg];
             const int32_t rows = page < 0 ? 0 : min(max(lim - (k0 + pg * 16), 0), 16);
             const int64_t off = page < 0 ? 0 : ((int64_t)page * p.hkv + kvh) * (16 * D);
-            kd[pg] = buf_desc(p.k_pool + off, rows * D * 2);
-            vd[pg] = buf_desc(p.v16_pool + off, rows > 0 ? 16 * D * 2 : 0);
+            ds.kd[pg] = buf_desc(p.k_pool + off, rows * D * 2);
+            ds.vd[pg] = buf_desc(p.v16_pool + off, rows > 0 ? 16 * D * 2 : 0);
         }
         // The descriptors may come from VALU writes of SGPRs (readfirstlane);
         // a VMEM read of such an SGPR needs 5 wait states, which the compiler
         // does not insert for inline-asm operands.
         asm volatile("s_nop 4");
+    }
+
+    // Descriptors with no records: copies through them write zeros.
+    __device__ __forceinline__ void empty(Descs &ds) const {
+        const u32x4 z = {0u, 0u, 0u, RSRC_W3};
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const int b = j * 4 + wave;
+        for (int pg = 0; pg < G::PAGES; ++pg) ds.kd[pg] = ds.vd[pg] = z;
+    }
+
+    // Copy n of this wave's PER_TILE copies of a tile into the stage at LDS
+    // byte address st: n < NB is K block 4n + w, the rest V blocks.
+    __device__ __forceinline__ void copy(const Descs &ds, uint32_t st, int n) const {
+        if (n < NB) {
+            const int j = n, b = j * 4 + wave;
             u32x4 dk;
             // page of K block b = (4j + w) * RB / 16: j*RB/4 for RB <= 4 (w < 4),
             // 2j + w/2 for RB = 8 (D = 64)
             if constexpr (RB <= 4)
-                dk = kd[(j * RB) / 4];
+                dk = ds.kd[(j * RB) / 4];
             else
-                dk = (wave >> 1) ? kd[2 * j + 1] : kd[2 * j];
+                dk = (wave >> 1) ? ds.kd[2 * j + 1] : ds.kd[2 * j];
             lds_copy16(dk, __builtin_amdgcn_readfirstlane(st + b * 1024), koff[j]);
-        }
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const int b = j * 4 + wave;
+        } else {
+            const int j = n - NB, b = j * 4 + wave;
             u32x4 dv;
             if constexpr (D >= 128)
-                dv = vd[(j * 4 * 32) / D];
+                dv = ds.vd[(j * 4 * 32) / D];
             else
-                dv = (wave >> 1) ? vd[2 * j + 1] : vd[2 * j];
+                dv = (wave >> 1) ? ds.vd[2 * j + 1] : ds.vd[2 * j];
             lds_copy16(dv, __builtin_amdgcn_readfirstlane(st + G::K_ELEMS * 2 + b * 1024), voff[j]);
         }
+    }
+
+    // All copies of tile keys [k0, k0 + KT) into the stage at LDS byte address st.
+    __device__ __forceinline__ void issue(const KParams &p, const int32_t *pt, int32_t k0, int32_t lim, int32_t kvh,
+                                          uint32_t st) const {
+        Descs ds;
+        prepare(p, pt, k0, lim, kvh, ds);
+#pragma unroll
+        for (int n = 0; n < PER_TILE; ++n) copy(ds, st, n);
     }
 };
 
@@ -465,11 +486,17 @@ struct RegLoader {
 };
 
 // pt[i] = page id of page index seg_p0 + i, or -1 at and past p_end.
+// (All loads first, then all LDS writes: one memory round trip, not four.)
 __device__ __forceinline__ void load_segment(const int32_t *bt_b, int32_t seg_p0, int32_t p_end, int32_t *pt) {
-    for (int i = threadIdx.x; i < SEG_PAGES; i += 256) {
-        const int32_t pi = seg_p0 + i;
-        pt[i] = pi < p_end ? page_of(bt_b, pi * 16) : -1;
+    static_assert(SEG_PAGES % 256 == 0, "segment must split evenly over the workgroup");
+    int32_t v[SEG_PAGES / 256];
+#pragma unroll
+    for (int k = 0; k < SEG_PAGES / 256; ++k) {
+        const int32_t pi = seg_p0 + (int)threadIdx.x + k * 256;
+        v[k] = pi < p_end ? page_of(bt_b, pi * 16) : -1;
     }
+#pragma unroll
+    for (int k = 0; k < SEG_PAGES / 256; ++k) pt[threadIdx.x + k * 256] = v[k];
 }
 
 template <int D, int MASK, int LD, bool QF32>
@@ -597,17 +624,28 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     DmaPlan<D> dma;
     if constexpr (LD == LD_DMA) dma.init();
     const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
+    // LDS table offset of tile tt's page ids, reloading the next segment when
+    // tt leaves the current one (a uniform call with a barrier; every wave is
+    // past its last read of the old segment: the previous tile ended with a
+    // barrier).
+    auto seg_index = [&](int32_t tt) {
+        int32_t pi = tt * G::PAGES - seg_p0;
+        if (pi + G::PAGES > SEG_PAGES) {
+            seg_p0 = tt * G::PAGES;
+            load_segment(bt_b, seg_p0, p_end, pt);
+            __syncthreads();
+            pi = 0;
+        }
+        return pi;
+    };
+    // Starts the transfer of tile tt into stage si (a uniform call).  DMA
+    // writes the stage directly; the register paths fill l, which l.store()
+    // writes out.
     auto issue = [&](RegLoader<D, VALID> &l, int32_t tt, int si) {
         if constexpr (LD == LD_VALID) {
             l.issue_valid(p, valid_b, bt_b, tt * G::KT, nk, kvh);
         } else {
-            int32_t pi = tt * G::PAGES - seg_p0;
-            if (pi + G::PAGES > SEG_PAGES) {
-                seg_p0 = tt * G::PAGES;
-                load_segment(bt_b, seg_p0, p_end, pt);
-                __syncthreads();
-                pi = 0;
-            }
+            const int32_t pi = seg_index(tt);
             if constexpr (LD == LD_DMA)
                 dma.issue(p, pt + pi, tt * G::KT, lim, kvh, smem_lds + si * (G::STAGE * 2));
             else
@@ -629,12 +667,61 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
         }
     };
 
+    // Mask of the tile starting at key k0 (raw score units).
+    auto apply_mask = [&](f32x16(&sv)[G::KB], int32_t k0) {
+        bool tile_full = k0 + G::KT <= nk;
+        if (MASK == EMB_MASK_CHUNK) tile_full = tile_full && k0 >= full_lo && k0 + G::KT <= full_hi;
+        if (MASK == EMB_MASK_TOKEN || MASK == EMB_MASK_ADD || MASK == EMB_MASK_BLOCKMAP) tile_full = false;
+        if (!tile_full) {  // one uniform branch around the whole per-key mask
+#pragma unroll
+            for (int kb = 0; kb < G::KB; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float x = sv[kb][r];
+                    const int32_t j = k0 + kb * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                    bool vis = row_ok && j < nk;
+                    if (MASK == EMB_MASK_CHUNK) {
+                        const int32_t qc = qpos / p.chunk, kc = j / p.chunk;
+                        vis = vis && kc <= qc && (p.window < 0 || qc - kc <= p.window);
+                    } else if (MASK == EMB_MASK_TOKEN) {
+                        vis = vis && reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                              (int64_t)tok * p.mask_q_stride + j] != 0;
+                    } else if (MASK == EMB_MASK_ADD) {
+                        if (vis)
+                            x += p.inv_scale * reinterpret_cast<const float *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                                      (int64_t)tok * p.mask_q_stride + j];
+                    } else if (MASK == EMB_MASK_BLOCKMAP) {
+                        vis = vis && p.bmap[(int64_t)b * p.bmap_b_stride + (int64_t)(tok / p.bsize) * p.bmap_cols +
+                                            j / p.bsize] != 0;
+                        if (vis && p.mask)
+                            vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
+                                                                            (int64_t)tok * p.mask_q_stride + j] != 0;
+                    }
+                    sv[kb][r] = vis ? x : -INFINITY;
+                }
+            }
+        }
+    };
+    // Row max of a tile (both half-waves hold the row's max).
+    auto tile_max = [&](const f32x16(&sv)[G::KB]) {
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < G::KB; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sv[kb][r]);
+        float a, c;
+        half_pair(mt, a, c);
+        return fmaxf(a, c);
+    };
+
     // Prologue: the first NST-1 tiles staged, S of tile t_lo computed.
     RegLoader<D, VALID> ld;
     if constexpr (LD == LD_DMA) {
-        load_q();  // in flight with the block-table fetch and the copies
+        // block table (one round trip), then the query loads and the copies
+        // back to back: the query lands while the copies are being issued
+        if (t_lo < t_hi) load_segment(bt_b, seg_p0, p_end, pt);
+        load_q();
         if (t_lo < t_hi) {
-            load_segment(bt_b, seg_p0, p_end, pt);
             __syncthreads();
             issue(ld, t_lo, 0);
             if (t_lo + 1 < t_hi) issue(ld, t_lo + 1, 1);
@@ -664,65 +751,52 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     __syncthreads();
     f32x16 s_cur[G::KB];
     if (wave_live) qk(smem, s_cur);
+    float mt_cur = -INFINITY;  // row max of the current tile (masked)
+    if (wave_live && t_lo < t_hi) {
+        apply_mask(s_cur, t_lo * G::KT);
+        mt_cur = tile_max(s_cur);
+    }
 
-    // Stage `cur` holds tile t, nx1 tile t+1, and the last stage receives
-    // tile t + NST - 1.  Past the end, the extra S and the stores work on
-    // stale stage contents that nothing reads.
+    // Stage `cur` holds tile t, nx1 tile t+1, and stage nxl receives tile
+    // t + NST - 1.  Past the end, the extra S and the stores work on stale
+    // stage contents that nothing reads.
+    //
+    // One key tile, per wave: the lazy rescale check on the row max of tile t;
+    // then the S MFMAs of tile t+1 with the softmax VALU work of tile t between
+    // them; then the P.V MFMAs of tile t with, between them, the copies of
+    // tile t+3 (DMA) and the mask and row max of tile t+1.  The order is fixed
+    // step by step (sched_barrier): each step issues one MFMA and the LDS read
+    // AHEAD steps later, so the MFMAs never wait out the LDS latency, and the
+    // copies trickle into the address unit instead of stalling all waves at
+    // once at the top of the tile.
+    constexpr int KS = D / 16;                 // k-steps of one 32-key S block
+    constexpr int NS = G::KB * KS;             // S MFMAs a tile
+    constexpr int NPV = G::KB * 2 * (D / 32);  // P.V MFMAs a tile
+    constexpr int EPM = G::KB * 16 / NS;       // score elements per step (both phases)
+    static_assert(NPV * EPM == G::KB * 16 && 2 * DmaPlan<D>::PER_TILE <= NPV, "tile schedule");
     int cur = 0;
     for (int32_t t = t_lo; t < t_hi; ++t) {
-        const int32_t k0 = t * G::KT;
         const int nx1 = cur + 1 == NST ? 0 : cur + 1;
         const int nxl = cur == 0 ? NST - 1 : cur - 1;  // receives tile t + NST - 1
         const bool more = t + NST - 1 < t_hi;
-        if (more) issue(ld, t + NST - 1, nxl);
+        typename DmaPlan<D>::Descs dsc;
+        const uint32_t st_l = smem_lds + nxl * (G::STAGE * 2);
+        if constexpr (LD == LD_DMA) {
+            // Past the last tile the copies still run, through empty
+            // descriptors: they write zeros into stage nxl, which no later
+            // tile reads, and keep the schedule free of branches.
+            if (more)
+                dma.prepare(p, pt + seg_index(t + NST - 1), (t + NST - 1) * G::KT, lim, kvh, dsc);
+            else
+                dma.empty(dsc);
+        } else {
+            if (more) issue(ld, t + NST - 1, nxl);
+        }
 
         if (wave_live) {
-            // mask (raw score units) and row max of tile t
-            bool tile_full = k0 + G::KT <= nk;
-            if (MASK == EMB_MASK_CHUNK) tile_full = tile_full && k0 >= full_lo && k0 + G::KT <= full_hi;
-            if (MASK == EMB_MASK_TOKEN || MASK == EMB_MASK_ADD || MASK == EMB_MASK_BLOCKMAP) tile_full = false;
-            if (!tile_full) {  // one uniform branch around the whole per-key mask
-#pragma unroll
-                for (int kb = 0; kb < G::KB; ++kb) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        float x = s_cur[kb][r];
-                        const int32_t j = k0 + kb * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-                        bool vis = row_ok && j < nk;
-                        if (MASK == EMB_MASK_CHUNK) {
-                            const int32_t qc = qpos / p.chunk, kc = j / p.chunk;
-                            vis = vis && kc <= qc && (p.window < 0 || qc - kc <= p.window);
-                        } else if (MASK == EMB_MASK_TOKEN) {
-                            vis = vis && reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
-                                                                                  (int64_t)tok * p.mask_q_stride + j] != 0;
-                        } else if (MASK == EMB_MASK_ADD) {
-                            if (vis)
-                                x += p.inv_scale * reinterpret_cast<const float *>(p.mask)[(int64_t)b * p.mask_b_stride +
-                                                                                          (int64_t)tok * p.mask_q_stride + j];
-                        } else if (MASK == EMB_MASK_BLOCKMAP) {
-                            vis = vis && p.bmap[(int64_t)b * p.bmap_b_stride + (int64_t)(tok / p.bsize) * p.bmap_cols +
-                                                j / p.bsize] != 0;
-                            if (vis && p.mask)
-                                vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride +
-                                                                                (int64_t)tok * p.mask_q_stride + j] != 0;
-                        }
-                        s_cur[kb][r] = vis ? x : -INFINITY;
-                    }
-                }
-            }
-            float mt = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < G::KB; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s_cur[kb][r]);
-            {
-                float a, c;
-                half_pair(mt, a, c);
-                mt = fmaxf(a, c);
-            }
             // wave-uniform lazy rescale
-            if (__builtin_amdgcn_ballot_w64(mt > m_run + p.th_raw) != 0) {
-                const float m_new = fmaxf(m_run, mt);
+            if (__builtin_amdgcn_ballot_w64(mt_cur > m_run + p.th_raw) != 0) {
+                const float m_new = fmaxf(m_run, mt_cur);
                 const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
 #pragma unroll
                 for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
@@ -730,15 +804,6 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                 m_run = m_new;
             }
 
-            // S of tile t+1 (MFMA) alongside P of tile t (VALU), then
-            // O^T += V^T P^T of tile t (MFMA, one 16-key page a step).  The
-            // order is fixed step by step (sched_barrier): each step issues one
-            // MFMA, the LDS read AHEAD steps later, and (S phase) 256/D softmax
-            // elements, whose VALU work runs while the MFMA executes.
-            constexpr int KS = D / 16;              // k-steps of one 32-key S block
-            constexpr int NS = G::KB * KS;          // S MFMAs a tile
-            constexpr int NPV = G::KB * 2 * (D / 32);  // P.V MFMAs a tile
-            constexpr int EPM = G::KB * 16 / NS;    // softmax elements per S step
             const uint16_t *stk = smem + nx1 * G::STAGE;
             const uint16_t *stv = smem + cur * G::STAGE;
             auto read_k = [&](int i) {
@@ -773,6 +838,8 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
+            if (t + 1 < t_hi) apply_mask(s_nxt, (t + 1) * G::KT);
+            float mt_nxt = -INFINITY;
             u32x4 vbuf[AHEAD];
 #pragma unroll
             for (int i = 0; i < AHEAD; ++i) vbuf[i] = read_v(i);
@@ -783,14 +850,31 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                 acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vbuf[i % AHEAD]),
                                                                   pf[kp >> 1][kp & 1], acc_o[dt], 0, 0, 0);
                 if (i + AHEAD < NPV) vbuf[i % AHEAD] = read_v(i + AHEAD);
+                if constexpr (LD == LD_DMA)
+                    if ((i & 1) && (i >> 1) < DmaPlan<D>::PER_TILE) dma.copy(dsc, st_l, i >> 1);
+#pragma unroll
+                for (int u = 0; u < EPM; ++u) {
+                    const int el = i * EPM + u;
+                    mt_nxt = fmaxf(mt_nxt, s_nxt[el / 16][el % 16]);
+                }
                 __builtin_amdgcn_sched_barrier(0);
+            }
+            {
+                float a, c;
+                half_pair(mt_nxt, a, c);
+                mt_cur = fmaxf(a, c);
             }
 #pragma unroll
             for (int kb = 0; kb < G::KB; ++kb) s_cur[kb] = s_nxt[kb];
-        }  // wave_live
+        } else if constexpr (LD == LD_DMA) {
+#pragma unroll
+            for (int n = 0; n < DmaPlan<D>::PER_TILE; ++n) dma.copy(dsc, st_l, n);
+        }
         if constexpr (LD == LD_DMA) {
-            // tile t+2 (needed by the next S) has landed; tile t+3 may still fly
-            if (more)
+            // tile t+2 (needed by the next S) has landed; tile t+3 may still
+            // fly; after the last tile nothing may (the epilogue reuses the
+            // stages)
+            if (t + 1 < t_hi)
                 wait_vmcnt<DmaPlan<D>::PER_TILE>();
             else
                 wait_vmcnt<0>();
