@@ -181,7 +181,7 @@ class PagedLayers:
         return b
 
 
-def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 4, 8)):
+def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
     n_layers, n_pref, n_new, hq, hkv, d = 18, 816, 51, 8, 1, 256
     P = PagedLayers(c, 0xE3BD0000, [n_pref] * n_layers, n_new, hq, hkv, d, n_steps=10)
     scale = 1.0 / math.sqrt(d)
@@ -285,7 +285,13 @@ def bench_cfg2(c: Ctx, steps, warmup):
     torch, emb = c.torch, c.emb
     L, n, hq, hkv, d = 18, 816, 8, 1, 256
     P = PagedLayers(c, 0xE3BD0001, [0] * L, n, hq, hkv, d, n_steps=1)
-    P.set_splits(1)
+    sweep = {}
+    for sp in (1, 2):
+        P.set_splits(sp)
+        ms_s, _ = c.time_graph(lambda st: P.attend(0, st, 1 / 16), steps, warmup)
+        sweep[sp] = ms_s * 1e3
+    best = min(sweep, key=sweep.get)
+    P.set_splits(best)
 
     def one(st):
         P.append(0, st)
@@ -294,7 +300,7 @@ def bench_cfg2(c: Ctx, steps, warmup):
     ms_a, _ = c.time_graph(lambda st: P.attend(0, st, 1 / 16), steps, warmup)
     fl = P.attn_flops()
     return dict(us_per_prefill=ms * 1e3, attn_us=ms_a * 1e3, attn_tflops=fl / (ms_a * 1e-3) / 1e12,
-                mfma_frac=fl / (ms_a * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, flops=fl)
+                mfma_frac=fl / (ms_a * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, flops=fl, splits=best, split_sweep_us=sweep)
 
 
 def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
@@ -327,6 +333,14 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
     # the slot range the evicted oldest chunk held (chunk 0), reused by the new chunk
     new_slots = c.i32(np.arange(C))
     scale = 1 / math.sqrt(d)
+    cur_split = [1, None]  # splits, workspace
+
+    def set_split(sp):
+        cur_split[0] = sp
+        cur_split[1] = None
+        if sp > 1:
+            nb = emb.attn_workspace_bytes(1, C, H, H, d, sp)
+            cur_split[1] = torch.empty(nb // 4 + 64, dtype=torch.float32, device=c.dev)
 
     def layer(l, st, append=True):
         kp, vp, v16, bt = pools[l]
@@ -334,13 +348,21 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
             emb.kv_append(knew, vnew, H * d, C, new_slots, bt, cap, kp, vp, H, d, stream=st, v16_pool=v16)
         emb.paged_attention(q=q, out=out, k_pool=kp, v_pool=vp, v16_pool=v16, batch=1, hq=H, hkv=H, d=d, max_q=C,
                             scale=scale, capacity=cap, cu_q=cu, n_keys=nk, block_tables=bt, bt_stride=pages,
-                            stream=st)
+                            splits=cur_split[0], workspace=cur_split[1], stream=st)
 
     if eager_only:  # profiling: plain launches of the attention kernel
+        set_split(4)
         for i in range(warmup + steps):
             layer(i % n_layers, c.stream, False)
         torch.cuda.synchronize()
         return {}
+    sweep = {}
+    for sp in (1, 2, 3, 4, 6):
+        set_split(sp)
+        ms_s, _ = c.time_graph(lambda st: [layer(l, st, False) for l in range(min(4, n_layers))], 3, 1)
+        sweep[sp] = ms_s * 1e3 / min(4, n_layers)
+    best = min(sweep, key=sweep.get)
+    set_split(best)
     ms_step, _ = c.time_graph(lambda st: [layer(l, st) for l in range(n_layers)], max(2, steps // 4), 1)
     ms_attn, _ = c.time_graph(lambda st: [layer(l, st, False) for l in range(n_layers)], max(2, steps // 4), 1)
     fl_layer = 4.0 * C * H * cap * d
@@ -350,7 +372,7 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
     return dict(ms_per_step=ms_step, attn_ms_per_step=ms_attn, attn_us_per_layer=attn_layer_us,
                 attn_tflops=fl_layer / (attn_layer_us * 1e-6) / 1e12,
                 mfma_frac=fl_layer / (attn_layer_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS,
-                flops_per_layer=fl_layer, layers=n_layers)
+                flops_per_layer=fl_layer, layers=n_layers, splits=best, split_sweep_us_per_layer=sweep)
 
 
 def _bf16_bits(f: np.ndarray) -> np.ndarray:
@@ -403,11 +425,14 @@ def bench_cfg5(c: Ctx, steps, warmup):
     def fused(st):
         emb.w8a16_qkv_append(x, qw, sc, M, K, H * d, qo, slots, bt, cap, kp, vp, H, d, stream=st, v16_pool=v16)
 
+    att_splits = 4  # the config-3 attention's best split on MI355X
+    ws = torch.empty(emb.attn_workspace_bytes(1, C, H, H, d, att_splits) // 4 + 64, dtype=torch.float32, device=c.dev)
+
     def step(st):
         fused(st)
         emb.paged_attention(q=qo, out=out, k_pool=kp, v_pool=vp, v16_pool=v16, batch=1, hq=H, hkv=H, d=d, max_q=C,
                             scale=1 / math.sqrt(d), capacity=cap, cu_q=cu, n_keys=nk, block_tables=bt,
-                            bt_stride=pages, stream=st)
+                            bt_stride=pages, splits=att_splits, workspace=ws, stream=st)
     ms_f, _ = c.time_graph(fused, steps, warmup)
     ms_s, _ = c.time_graph(step, max(2, steps // 4), 2)
     gemm_bytes = M * K * 2 + K * N + N * 2 + M * N * 2

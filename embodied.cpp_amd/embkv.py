@@ -44,6 +44,13 @@ class AttnArgs(C.Structure):
     ]
 
 
+EMB_GGML_F32, EMB_GGML_F16, EMB_GGML_BF16 = 0, 1, 30
+
+
+class GgmlTensor(C.Structure):
+    _fields_ = [("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4), ("data", vp)]
+
+
 _SIGS = {
     "emb_last_error": (C.c_char_p, []),
     "emb_version": (C.c_char_p, []),
@@ -97,6 +104,12 @@ _SIGS = {
     "lingbot_runtime_kv_attn_cublas_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int,
                                                      C.c_int, C.c_int, C.c_int, C.c_float, vp]),
     "emb_synth_normal_bf16": (C.c_int, [C.c_uint64, C.c_int64, u16p]),
+    "lingbot_flex_attn_f32": (C.c_int, [vp, vp, vp, vp, vp, vp] + [C.c_int] * 5 + [C.c_float, vp]),
+    "lingbot_flex_attn_f32_masked": (C.c_int, [vp, vp, vp, vp, vp, vp, vp] + [C.c_int] * 5 + [C.c_float, vp]),
+    "lingbot_flex_attn_cuda_smoke": (C.c_int, [vp]),
+    "emb_ggml_flash_attn_ext_workspace": (C.c_size_t, [C.POINTER(GgmlTensor)] * 5),
+    "emb_ggml_flash_attn_ext": (C.c_int, [C.POINTER(GgmlTensor)] * 4 + [C.c_float] * 3 +
+                                [C.POINTER(GgmlTensor), vp, C.c_size_t, vp]),
     "emb_w8a16_gemm": (C.c_int, [vp, C.c_int32, C.c_int64, vp, vp, C.c_int32, C.c_int32, C.c_int32,
                                  vp, C.c_int64, C.c_int32, vp]),
     "emb_w8a16_qkv_append": (C.c_int, [vp, C.c_int32, C.c_int64, vp, vp, C.c_int32, C.c_int32,
@@ -328,3 +341,50 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
     a.block_map_batch_stride = block_map_batch_stride
     a.splits = splits; a.workspace = ptr(workspace)
     return check(lib().emb_paged_attention(C.byref(a), stream_ptr(stream)), "emb_paged_attention")
+
+
+def flex_attention(q, k, v, row_ptr, col_idx, out, seq_q, seq_k, n_heads, head_dim, block_size, scale,
+                   token_mask=None, stream=None):
+    """lingbot_flex_attn_f32[_masked]: f32 [seq][H][D] device tensors, device CSR."""
+    L = lib()
+    if token_mask is None:
+        rc = L.lingbot_flex_attn_f32(ptr(q), ptr(k), ptr(v), ptr(row_ptr), ptr(col_idx), ptr(out), seq_q, seq_k,
+                                     n_heads, head_dim, block_size, scale, stream_ptr(stream))
+    else:
+        rc = L.lingbot_flex_attn_f32_masked(ptr(q), ptr(k), ptr(v), ptr(row_ptr), ptr(col_idx), ptr(token_mask),
+                                            ptr(out), seq_q, seq_k, n_heads, head_dim, block_size, scale,
+                                            stream_ptr(stream))
+    return check(rc, "lingbot_flex_attn_f32")
+
+
+def ggml_tensor(t, ggml_type, ne, nb_elems=None):
+    """Descriptor of a device tensor: ne innermost-first; nb_elems (element
+    strides, innermost first) default to the contiguous ones."""
+    es = 4 if ggml_type == EMB_GGML_F32 else 2
+    ne = list(ne) + [1] * (4 - len(ne))
+    if nb_elems is None:
+        nb_elems = [1, ne[0], ne[0] * ne[1], ne[0] * ne[1] * ne[2]]
+    d = GgmlTensor()
+    d.type = ggml_type
+    for i in range(4):
+        d.ne[i] = int(ne[i])
+        d.nb[i] = int(nb_elems[i]) * es
+    d.data = ptr(t)
+    return d
+
+
+def ggml_flash_attn_ext(q, k, v, mask, dst, scale, workspace=None, max_bias=0.0, logit_softcap=0.0,
+                        stream=None):
+    """emb_ggml_flash_attn_ext over GgmlTensor descriptors (mask may be None).
+    Allocates the workspace with torch when none is given."""
+    L = lib()
+    mp = C.byref(mask) if mask is not None else None
+    nbytes = L.emb_ggml_flash_attn_ext_workspace(C.byref(q), C.byref(k), C.byref(v), mp, C.byref(dst))
+    if nbytes == 0:
+        raise RuntimeError("emb_ggml_flash_attn_ext: descriptors rejected")
+    if workspace is None:
+        import torch
+        workspace = torch.empty(nbytes // 4 + 64, dtype=torch.float32, device="cuda")
+    rc = L.emb_ggml_flash_attn_ext(C.byref(q), C.byref(k), C.byref(v), mp, scale, max_bias, logit_softcap,
+                                   C.byref(dst), ptr(workspace), nbytes, stream_ptr(stream))
+    return check(rc, "emb_ggml_flash_attn_ext")

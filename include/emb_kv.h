@@ -238,6 +238,71 @@ int lingbot_runtime_kv_attn_cublas_f32(const float *q, const float *cache_k,
                                        int capacity, float scale, hipStream_t stream);
 
 /* ============================================================
+ * Whole-tensor faces: K/V given as tensors are staged by the library into an
+ * identity-paged bf16 pool with its f16 V shadow, then attended with
+ * emb_paged_attention.  Head sizes up to 256 other than 64/128/256 run padded
+ * with zero dimensions (which change no score and no kept output).
+ * ============================================================ */
+
+/* Block-sparse attention, same signatures as
+ * kernels/lingbot/lingbot_flex_attn_cuda.h:13-43 with hipStream_t: query q of
+ * block qb = q / block_size sees the keys of the key blocks listed in
+ * col_idx[row_ptr[qb] .. row_ptr[qb+1]) (device CSR), filtered by token_mask
+ * (u8 [seq_q][seq_k], masked variant); out = softmax(scale q.k) v, 0 for a
+ * row with no visible key.  q/k/v/out: f32 [seq][n_heads][head_dim], device.
+ * A key block listed twice counts once (the reference would count it twice).
+ * Q and K round to bf16, P and V to f16 (fp32 accumulation).  These two own a
+ * device workspace (hipMalloc when a call needs more than the last one,
+ * kept until exit): the first call at a new size must not be under stream
+ * capture, and calls on one device from several threads must not overlap. */
+int lingbot_flex_attn_f32(const float *q, const float *k, const float *v, const int *row_ptr,
+                          const int *col_idx, float *out, int seq_q, int seq_k, int n_heads,
+                          int head_dim, int block_size, float scale, hipStream_t stream);
+int lingbot_flex_attn_f32_masked(const float *q, const float *k, const float *v,
+                                 const int *row_ptr, const int *col_idx,
+                                 const unsigned char *token_mask, float *out, int seq_q,
+                                 int seq_k, int n_heads, int head_dim, int block_size,
+                                 float scale, hipStream_t stream);
+/* The reference's in-source known-answer test (lingbot_flex_attn_cuda.cu:
+ * 1010-1076): its 8-token, 2-head, head-size-8 inputs, causal window-4 mask
+ * and CSR {0,1,3}/{0,0,1}, checked against a dense host loop.  Returns 0 when
+ * the max abs difference is below 2e-2 (the reference's own bound is 1e-5
+ * for its all-f32 kernel) and prints it.  Allocates its small device inputs. */
+int lingbot_flex_attn_cuda_smoke(hipStream_t stream);
+
+/* ggml tensor descriptor (the fields a ggml-hip backend forwards). */
+enum { EMB_GGML_F32 = 0, EMB_GGML_F16 = 1, EMB_GGML_BF16 = 30 }; /* ggml_type values */
+typedef struct emb_ggml_tensor {
+    int32_t type;      /* EMB_GGML_F32 / F16 / BF16 */
+    int64_t ne[4];     /* elements per dimension, ne[0] innermost */
+    size_t nb[4];      /* byte strides */
+    void *data;        /* device memory */
+} emb_ggml_tensor;
+
+/* ggml_flash_attn_ext(q, k, v, mask, scale, max_bias, logit_softcap) with
+ * F32 precision, as the VLA experts call it (models/hy_vla.cpp:1066-1076;
+ * the MUL_MAT -> SOFT_MAX_EXT -> MUL_MAT pattern of models/pi05.cpp:405-418
+ * is the same computation with dst strides [D, n_q, H_q]):
+ *   q [D, n_q, H_q, B], k/v [D, n_kv, H_kv, B or 1] (v not transposed),
+ *   mask (may be NULL) additive [n_kv, >= n_q, 1, 1 or B], F16 or F32,
+ *   dst F32 [D, H_q, n_q, B] at any strides,
+ *   dst = softmax(scale * q.k + mask) v, q head h reading kv head
+ *   h / (H_q / H_kv).  max_bias and logit_softcap must be 0 (-4 otherwise).
+ * Q.K^T runs as bf16 MFMA: f32/f16 q and k round to bf16 (f16 v is kept
+ * exactly for P.V), so the result is that of the reference on bf16-rounded q
+ * and k, within the attention tolerance. 
+ * workspace: device memory of emb_ggml_flash_attn_ext_workspace() bytes (16-
+ * byte aligned); nothing is allocated.  The workspace query returns 0 for
+ * descriptors the entry would reject. */
+size_t emb_ggml_flash_attn_ext_workspace(const emb_ggml_tensor *q, const emb_ggml_tensor *k,
+                                         const emb_ggml_tensor *v, const emb_ggml_tensor *mask,
+                                         const emb_ggml_tensor *dst);
+int emb_ggml_flash_attn_ext(const emb_ggml_tensor *q, const emb_ggml_tensor *k,
+                            const emb_ggml_tensor *v, const emb_ggml_tensor *mask, float scale,
+                            float max_bias, float logit_softcap, emb_ggml_tensor *dst,
+                            void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ============================================================
  * W8A16 linear (int8 weight-only, Marlin kU8B128 channelwise layout)
  * y[m][n] = bf16( (sum_k bf16(x[m][k]) * (u8[k][n] - 128)) * s[n] ), fp32
  * accumulate, the scale applied to the fp32 accumulator -- the numerics of

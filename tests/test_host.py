@@ -174,3 +174,21 @@ def test_device_entry_points_reject_bad_arguments(emb):
                             max_q=4, scale=0.1, capacity=64, splits=4)
     assert L.lingbot_runtime_kv_attn_f32(None, None, None, None, None, 1, 1, 1, 64, 0.1, None) == -1
     assert emb.attn_workspace_bytes(1, 51, 8, 1, 256, 4) == 4 * 512 * (256 + 2) * 4
+    # whole-tensor faces: null pointers, head sizes past 256, ggml descriptors
+    assert L.lingbot_flex_attn_f32(None, buf, buf, buf, buf, buf, 8, 8, 2, 64, 4, 0.1, None) == -1
+    assert L.lingbot_flex_attn_f32(buf, buf, buf, buf, buf, buf, 8, 8, 2, 320, 4, 0.1, None) == -4
+    assert L.lingbot_flex_attn_f32_masked(buf, buf, buf, buf, buf, None, buf, 8, 8, 2, 64, 4, 0.1, None) == -1
+    q = emb.ggml_tensor(256, emb.EMB_GGML_F32, [128, 5, 8, 2])
+    k = emb.ggml_tensor(256, emb.EMB_GGML_F16, [128, 40, 2, 2])
+    o = emb.ggml_tensor(256, emb.EMB_GGML_F32, [128, 8, 5, 2])
+    ws = L.emb_ggml_flash_attn_ext_workspace(C.byref(q), C.byref(k), C.byref(k), None, C.byref(o))
+    pages = (40 + 15) // 16
+    assert ws >= 3 * 2 * pages * 2 * 16 * 128 * 2  # three pools of two sequences
+    o_bad = emb.ggml_tensor(256, emb.EMB_GGML_F32, [128, 5, 8, 2])  # not [D, H_q, n_q, B]
+    assert L.emb_ggml_flash_attn_ext_workspace(C.byref(q), C.byref(k), C.byref(k), None, C.byref(o_bad)) == 0
+    q_big = emb.ggml_tensor(256, emb.EMB_GGML_F32, [320, 5, 8, 2])
+    k_big = emb.ggml_tensor(256, emb.EMB_GGML_F16, [320, 40, 2, 2])
+    assert L.emb_ggml_flash_attn_ext_workspace(C.byref(q_big), C.byref(k_big), C.byref(k_big), None, None) == 0
+    assert L.emb_ggml_flash_attn_ext(C.byref(q), C.byref(k), C.byref(k), None, 0.1, 0.0, 0.0, C.byref(o),
+                                     None, ws, None) == -1  # no workspace
+    assert "workspace" in emb.last_error()
