@@ -144,7 +144,7 @@ class PagedLayers:
         self.splits = splits
         if splits > 1:
             nb = self.c.emb.attn_workspace_bytes(self.L, self.n_new, self.hq, self.hkv, self.d, splits)
-            self.ws = self.c.torch.empty(nb // 4 + 64, dtype=self.c.torch.float32, device=self.c.dev)
+            self.ws = self.c.torch.zeros(nb // 4 + 64, dtype=self.c.torch.float32, device=self.c.dev)
 
     def append(self, step, stream):
         s = step % self.n_steps
@@ -340,7 +340,7 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
         cur_split[1] = None
         if sp > 1:
             nb = emb.attn_workspace_bytes(1, C, H, H, d, sp)
-            cur_split[1] = torch.empty(nb // 4 + 64, dtype=torch.float32, device=c.dev)
+            cur_split[1] = torch.zeros(nb // 4 + 64, dtype=torch.float32, device=c.dev)
 
     def layer(l, st, append=True):
         kp, vp, v16, bt = pools[l]
@@ -426,7 +426,7 @@ def bench_cfg5(c: Ctx, steps, warmup):
         emb.w8a16_qkv_append(x, qw, sc, M, K, H * d, qo, slots, bt, cap, kp, vp, H, d, stream=st, v16_pool=v16)
 
     att_splits = 4  # the config-3 attention's best split on MI355X
-    ws = torch.empty(emb.attn_workspace_bytes(1, C, H, H, d, att_splits) // 4 + 64, dtype=torch.float32, device=c.dev)
+    ws = torch.zeros(emb.attn_workspace_bytes(1, C, H, H, d, att_splits) // 4 + 64, dtype=torch.float32, device=c.dev)
 
     def step(st):
         fused(st)
@@ -524,6 +524,69 @@ def cpu_baseline(target_s=10.0):
     }
 
 
+TRAFFIC_FILE = "paged_attn_cfg1_traffic.md"
+COPY_CALIB_BYTES = 256 << 20
+
+
+def _pmc_kib_per_dispatch(path: Path, kernel_sub: str, counter: str) -> float:
+    """Mean per-dispatch value of one counter over the dispatches of kernels whose name contains kernel_sub."""
+    import csv
+    f = next(path.rglob("*counter_collection.csv"))
+    vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(f))
+            if kernel_sub in r["Kernel_Name"] and r["Counter_Name"] == counter]
+    if not vals:
+        raise RuntimeError(f"{f}: no {counter} rows for {kernel_sub}")
+    return sum(vals) / len(vals)
+
+
+def traffic_summary(root: Path):
+    """HBM bytes per launch of the config-1 attention kernel from FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch), each scaled by what the same counter reads for a plain device copy of known size."""
+    fa = _pmc_kib_per_dispatch(root / "pmc_fetch_attn", "paged_attn_kernel", "FETCH_SIZE")
+    wa = _pmc_kib_per_dispatch(root / "pmc_write_attn", "paged_attn_kernel", "WRITE_SIZE")
+    fc = _pmc_kib_per_dispatch(root / "pmc_fetch_copy", "copyBuffer", "FETCH_SIZE")
+    wc = _pmc_kib_per_dispatch(root / "pmc_write_copy", "copyBuffer", "WRITE_SIZE")
+    kf, kw = fc * 1024 / COPY_CALIB_BYTES, wc * 1024 / COPY_CALIB_BYTES
+    traffic = fa * 1024 / kf + wa * 1024 / kw
+    cmd = ("cd /tmp && timeout -s KILL 90 rocprofv3 --pmc {C} --output-format csv -d <dir>/pmc_{c}_{w} -o run "
+           "-- python3 /root/repo/bench.py --only {W} --steps 20 --warmup 2")
+    text = f"""# Config-1 attention kernel: HBM traffic per launch (rocprofv3 PMC)
+
+Kernel: `paged_attn_kernel<256, FULL, DMA>` (config 1: 18 layers x 51 queries x 8 heads over 867 keys,
+head_dim 256, split-K 3), launched by `bench.py --only cfg1_attn`.
+
+| pass | command | mean per dispatch |
+|---|---|---|
+| FETCH_SIZE, attention | `{cmd.format(C="FETCH_SIZE", c="fetch", w="attn", W="cfg1_attn")}` | {fa:.1f} KiB |
+| WRITE_SIZE, attention | `{cmd.format(C="WRITE_SIZE", c="write", w="attn", W="cfg1_attn")}` | {wa:.1f} KiB |
+| FETCH_SIZE, copy | `{cmd.format(C="FETCH_SIZE", c="fetch", w="copy", W="copy_calib")}` | {fc:.1f} KiB |
+| WRITE_SIZE, copy | `{cmd.format(C="WRITE_SIZE", c="write", w="copy", W="copy_calib")}` | {wc:.1f} KiB |
+
+Calibration: the copy moves {COPY_CALIB_BYTES >> 20} MiB each way, so FETCH_SIZE reads {kf:.4f}x and
+WRITE_SIZE {kw:.4f}x the true bytes.
+
+traffic_bytes_per_launch: {traffic:.0f}
+
+(Fetch {fa * 1024 / kf:.0f} B + write {wa * 1024 / kw:.0f} B after calibration; summary written by
+`python bench.py --traffic-summary <dir>`.)
+"""
+    out = ROOT / "profiles" / TRAFFIC_FILE
+    out.write_text(text)
+    print(text)
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed PMC summary, or None."""
+    f = ROOT / "profiles" / TRAFFIC_FILE
+    try:
+        for line in f.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -531,8 +594,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="cfg1,cfg2,cfg3,cfg4,cfg5")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="cfg1_attn: only the headline kernel loop (profiling)")
+    ap.add_argument("--only", default="",
+                    help="profiling targets: cfg1_attn (the headline kernel loop), cfg3_attn, cfg5_gemm, "
+                         "copy_calib (a plain 256 MiB device copy, the PMC byte-counter calibration)")
+    ap.add_argument("--traffic-summary", default="", metavar="DIR",
+                    help="write profiles/" + TRAFFIC_FILE + " from the four rocprofv3 --pmc runs under DIR "
+                         "(pmc_fetch_attn, pmc_write_attn, pmc_fetch_copy, pmc_write_copy) and exit")
     args = ap.parse_args()
+    if args.traffic_summary:
+        traffic_summary(Path(args.traffic_summary))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the attention step has no multi-GPU path here; see DESIGN.md for how it would shard)",
@@ -540,9 +611,17 @@ def main():
         sys.exit(2)
 
     c = Ctx()
+    if args.only == "copy_calib":
+        src = c.torch.ones(COPY_CALIB_BYTES // 4, dtype=c.torch.float32, device=c.dev)
+        dst = c.torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        c.torch.cuda.synchronize()
+        log("profile loop done")
+        return
     if args.only == "cfg1_attn":
         P = PagedLayers(c, 0xE3BD0000, [816] * 18, 51, 8, 1, 256, n_steps=10)
-        P.set_splits(int(os.environ.get("EMB_SPLITS", "2")))
+        P.set_splits(int(os.environ.get("EMB_SPLITS", "3")))
         for i in range(args.warmup + args.steps):
             P.attend(i, c.stream, 1 / 16)
         c.torch.cuda.synchronize()
@@ -608,8 +687,11 @@ def main():
                    "layers": 18, "prefix": 816, "queries": 51, "hq": 8, "hkv": 1, "head_dim": 256,
                    "page_tokens": 16, "splits": r1["splits"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
-                     "kernel": "paged_attn_kernel<256,FULL>", "kernel_us": kern_us,
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": read_traffic(),
+                     "kernel": ("paged_attn_kernel<256,FULL,DMA>" +
+                                (f" + attn_merge_kernel<256> (one split-K {r1['splits']} attention launch)"
+                                 if r1["splits"] > 1 else "")),
+                     "kernel_us": kern_us,
                      "bytes_per_launch": r1["attn_bytes_per_launch"]},
         "cpu_baseline": cpu,
         "extra": extra,

@@ -105,6 +105,8 @@ def test_pi05_action_expert_shape(emb, orc, torch_dev):
     assert_close(got, s.oracle(orc, 0, scale), "pi05 cfg1")
     got4 = s.run(emb, torch, dev, scale, splits=4)[0]
     assert_close(got4, s.oracle(orc, 0, scale), "pi05 cfg1 split-K 4")
+    got6 = s.run(emb, torch, dev, scale, splits=6)[0]
+    assert_close(got6, s.oracle(orc, 0, scale), "pi05 cfg1 split-K 6")
 
 
 def test_multi_session_sweep(emb, orc, torch_dev):
