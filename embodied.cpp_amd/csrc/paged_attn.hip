@@ -138,11 +138,21 @@ struct KParams {
     const uint8_t *bmap;
     int32_t bsize, bmap_cols;
     int64_t bmap_b_stride;
-    float *ws_o;   // [batch*hkv][splits][row_tiles*128][D]
-    float *ws_ml;  // [batch*hkv][splits][row_tiles*128][2]
+    uint16_t *ws_o;  // [batch*hkv][splits][row_tiles*128][D] f16: the split's O / l
+    float *ws_ml;    // [batch*hkv][splits][row_tiles*128][2]: m (log2 units), l
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+
+// Four floats as four f16 (round to nearest even), packed in two dwords.
+__device__ __forceinline__ u32x2 f16x4_bits(const f32x4 &v) {
+    u32x2 w;
+    w[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[0]) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[1]) << 16);
+    w[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2]) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[3]) << 16);
+    return w;
+}
 
 // Lane l and lane l ^ 32 of x, as a pair, by one VALU lane swap: the first
 // element is x of lane l & 31, the second x of lane l | 32 (so their max or
@@ -905,7 +915,10 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
         p.ws_ml[rowi * 2] = m_run == -INFINITY ? -INFINITY : m_run * p.c_log2;
         p.ws_ml[rowi * 2 + 1] = l_run;
     }
-    const float sc = partial ? 1.0f : (l_run > 0.0f ? 1.0f / l_run : 0.0f);
+    // (a split's partial is normalised too, and stored in f16: O/l of a split
+    // is a weighted mean of V rows, so f16 keeps 11 bits relative to each
+    // element; the merge reweights the splits by l)
+    const float sc = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     constexpr int CHR = D / 4;  // 16-byte chunks in a row of D floats
     if constexpr (NST * G::STAGE * 2 >= WAVES * ROWS_PER_WAVE * D * 4) {
         // every wave is past its last stage read (the loop ended with a barrier)
@@ -933,7 +946,6 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
         // lane r < 32 holds the destination (element offset) of row r of the
         // wave, -1 past the last row; a store takes its rows' offsets by lane
         // reads (scalar when one row fills the instruction)
-        float *const obase = partial ? p.ws_o : p.out;
         int64_t dst_off = -1;
         if (row_ok)
             dst_off = partial ? (unit_row0 + my_row) * D
@@ -955,33 +967,43 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
 #pragma unroll
                 for (int u = 1; u < RPI; ++u) off = sub == u ? cand[u] : off;
             }
-            if (off >= 0) *reinterpret_cast<f32x4 *>(obase + off + c * 4) = rv[i];
+            if (off < 0) continue;
+            if (partial)
+                *reinterpret_cast<u32x2 *>(p.ws_o + off + c * 4) = f16x4_bits(rv[i]);
+            else
+                *reinterpret_cast<f32x4 *>(p.out + off + c * 4) = rv[i];
         }
     } else {
         if (!row_ok) return;
-        float *dst = partial ? p.ws_o + (unit_row0 + my_row) * D
-                             : p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
+        const int64_t off = partial ? (unit_row0 + my_row) * D
+                                    : (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
                                  acc_o[dt][j * 4 + 3] * sc};
-                *reinterpret_cast<f32x4 *>(dst + dt * 32 + j * 8 + lhi * 4) = v;
+                const int64_t e = off + dt * 32 + j * 8 + lhi * 4;
+                if (partial)
+                    *reinterpret_cast<u32x2 *>(p.ws_o + e) = f16x4_bits(v);
+                else
+                    *reinterpret_cast<f32x4 *>(p.out + e) = v;
             }
     }
 }
 
-// Combines split partials (m in log2 units): m = max m_s, l = sum l_s 2^(m_s - m),
-// out = sum O_s 2^(m_s - m) / l.  One thread per (row, 4 dims).
-template <int D>
+// Combines split partials (m in log2 units, O_s already divided by l_s):
+// m = max m_s, w_s = l_s 2^(m_s - m), out = sum w_s O_s / sum w_s.  One thread
+// per (row, 8 dims); the loads of up to MS splits are all issued before any is
+// used (a loop over splits would wait out one memory round trip per split).
+template <int D, int MS>
 __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
     const int64_t rows_per_unit = (int64_t)p.row_tiles * ROWS_PER_WG;
-    const int64_t total = (int64_t)p.batch * p.hkv * rows_per_unit * (D / 4);
+    const int64_t total = (int64_t)p.batch * p.hkv * rows_per_unit * (D / 8);
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * blockDim.x) {
-        const int d4 = (int)(idx % (D / 4));
-        int64_t r = idx / (D / 4);
+        const int d8 = (int)(idx % (D / 8));
+        int64_t r = idx / (D / 8);
         const int32_t row = (int32_t)(r % rows_per_unit);
         r /= rows_per_unit;
         const int kvh = (int)(r % p.hkv);
@@ -990,25 +1012,37 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
         const int32_t nq = p.cu_q ? p.cu_q[b + 1] - q_begin : p.nq_single;
         if (row >= nq * p.G) continue;
         const int64_t unit0 = (int64_t)(b * p.hkv + kvh) * p.splits;
+        float ms[MS], ls[MS];
+        u32x4 os[MS];
+#pragma unroll
+        for (int s = 0; s < MS; ++s) {
+            const int64_t ri = (unit0 + (s < p.splits ? s : 0)) * rows_per_unit + row;
+            const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + ri * 2);
+            ms[s] = s < p.splits ? ml.x : -INFINITY;
+            ls[s] = ml.y;
+            os[s] = *reinterpret_cast<const u32x4 *>(p.ws_o + ri * D + d8 * 8);
+        }
         float m = -INFINITY;
-        for (int s = 0; s < p.splits; ++s) m = fmaxf(m, p.ws_ml[((unit0 + s) * rows_per_unit + row) * 2]);
-        const float m_use = m == -INFINITY ? 0.0f : m;
-        float l = 0.0f;
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < p.splits; ++s) {
-            const int64_t ri = (unit0 + s) * rows_per_unit + row;
-            const float w = __builtin_amdgcn_exp2f(p.ws_ml[ri * 2] - m_use);
-            l += w * p.ws_ml[ri * 2 + 1];
-            const f32x4 x = *reinterpret_cast<const f32x4 *>(p.ws_o + ri * D + d4 * 4);
-            o += w * x;
+#pragma unroll
+        for (int s = 0; s < MS; ++s) m = fmaxf(m, ms[s]);
+        float l = 0.0f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < MS; ++s) {
+            const float w = ms[s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[s] - m) * ls[s];
+            l += w;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                o[e] += w * (float)__builtin_bit_cast(_Float16, (uint16_t)(os[s][e >> 1] >> ((e & 1) * 16)));
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         const int32_t tok = row / p.G;
         const int32_t head = kvh * p.G + row % p.G;
-        *reinterpret_cast<f32x4 *>(p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + d4 * 4) =
-            o * inv;
+        float *dst = p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + d8 * 8;
+        *reinterpret_cast<f32x4 *>(dst) = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+        *reinterpret_cast<f32x4 *>(dst + 4) = f32x4{o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv};
     }
 }
+
 
 template <int D, int MASK, int LD, bool QF32>
 hipError_t launch_kernel(const KParams &kp, hipStream_t stream) {
@@ -1043,10 +1077,17 @@ hipError_t dispatch_mask(const KParams &kp, int mask, int ld, bool qf32, hipStre
 
 template <int D>
 hipError_t launch_merge(const KParams &kp, hipStream_t stream) {
-    const int64_t total = (int64_t)kp.batch * kp.hkv * kp.row_tiles * ROWS_PER_WG * (D / 4);
+    const int64_t total = (int64_t)kp.batch * kp.hkv * kp.row_tiles * ROWS_PER_WG * (D / 8);
     int64_t g = (total + 255) / 256;
     if (g > 65536) g = 65536;
-    hipLaunchKernelGGL((attn_merge_kernel<D>), dim3((int)g), dim3(256), 0, stream, kp);
+    if (kp.splits <= 4)
+        hipLaunchKernelGGL((attn_merge_kernel<D, 4>), dim3((int)g), dim3(256), 0, stream, kp);
+    else if (kp.splits <= 8)
+        hipLaunchKernelGGL((attn_merge_kernel<D, 8>), dim3((int)g), dim3(256), 0, stream, kp);
+    else if (kp.splits <= 16)
+        hipLaunchKernelGGL((attn_merge_kernel<D, 16>), dim3((int)g), dim3(256), 0, stream, kp);
+    else
+        hipLaunchKernelGGL((attn_merge_kernel<D, 64>), dim3((int)g), dim3(256), 0, stream, kp);
     return hipGetLastError();
 }
 
@@ -1121,8 +1162,8 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     kp.bmap_b_stride = a->block_map_batch_stride;
     if (splits > 1) {
         const int64_t rows_all = (int64_t)a->batch * a->hkv * splits * kp.row_tiles * ROWS_PER_WG;
-        kp.ws_o = (float *)a->workspace;
-        kp.ws_ml = kp.ws_o + rows_all * a->head_dim;
+        kp.ws_o = (uint16_t *)a->workspace;
+        kp.ws_ml = reinterpret_cast<float *>(kp.ws_o + rows_all * a->head_dim);
     }
     const int ld = a->valid_slots ? LD_VALID : (a->v16_pool ? LD_DMA : LD_REG);
     const bool qf32 = a->q_is_f32 != 0;
@@ -1178,7 +1219,7 @@ size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_
     if (batch <= 0 || max_q <= 0 || hq <= 0 || hkv <= 0 || hq % hkv || head_dim <= 0 || splits <= 1) return 0;
     const int64_t row_tiles = ((int64_t)max_q * (hq / hkv) + ROWS_PER_WG - 1) / ROWS_PER_WG;
     const int64_t rows_all = (int64_t)batch * hkv * splits * row_tiles * ROWS_PER_WG;
-    return (size_t)rows_all * (size_t)(head_dim + 2) * sizeof(float);
+    return (size_t)rows_all * ((size_t)head_dim * sizeof(uint16_t) + 2 * sizeof(float));
 }
 
 int emb_paged_attention(const emb_attn_args *a, hipStream_t stream) {

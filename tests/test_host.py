@@ -173,7 +173,8 @@ def test_device_entry_points_reject_bad_arguments(emb):
         emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=1, hq=8, hkv=1, d=128,
                             max_q=4, scale=0.1, capacity=64, splits=4)
     assert L.lingbot_runtime_kv_attn_f32(None, None, None, None, None, 1, 1, 1, 64, 0.1, None) == -1
-    assert emb.attn_workspace_bytes(1, 51, 8, 1, 256, 4) == 4 * 512 * (256 + 2) * 4
+    # f16 partial rows (O/l) plus f32 (m, l) per row
+    assert emb.attn_workspace_bytes(1, 51, 8, 1, 256, 4) == 4 * 512 * (256 * 2 + 2 * 4)
     # whole-tensor faces: null pointers, head sizes past 256, ggml descriptors
     assert L.lingbot_flex_attn_f32(None, buf, buf, buf, buf, buf, 8, 8, 2, 64, 4, 0.1, None) == -1
     assert L.lingbot_flex_attn_f32(buf, buf, buf, buf, buf, buf, 8, 8, 2, 320, 4, 0.1, None) == -4
