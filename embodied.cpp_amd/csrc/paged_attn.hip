@@ -82,6 +82,8 @@ constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
 constexpr float RESCALE_TH = 8.0f;  // log2 units
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int SEG_PAGES = 1024;
+// Block-table entries every wave of the DMA path holds in registers from the start.
+constexpr int WIN_PAGES = 128;
 // LDS fragment reads kept in flight ahead of the MFMA that consumes them: the
 // LDS latency is several MFMA issue slots, and the compiler's own schedule
 // issues each read just one MFMA ahead.
@@ -138,7 +140,10 @@ struct KParams {
     const uint8_t *bmap;
     int32_t bsize, bmap_cols;
     int64_t bmap_b_stride;
-    uint16_t *ws_o;  // [batch*hkv][splits][row_tiles*128][D] f16: the split's O / l
+    // [batch*hkv][splits][row_tiles*128][D] f16: the split's O / l, each
+    // 32-row block in the MFMA accumulator order (element ((c*64 + lane)*4 + e)
+    // of a block is dims c*8 + (lane/32)*4 + e of row lane%32)
+    uint16_t *ws_o;
     float *ws_ml;    // [batch*hkv][splits][row_tiles*128][2]: m (log2 units), l
 };
 
@@ -301,6 +306,10 @@ struct DmaPlan {
                                             Descs &ds) const {
         int32_t pid[G::PAGES];
         tile_pages<D>(pt, pid);
+        prepare_ids(p, pid, k0, lim, kvh, ds);
+    }
+    __device__ __forceinline__ void prepare_ids(const KParams &p, const int32_t (&pid)[G::PAGES], int32_t k0,
+                                                int32_t lim, int32_t kvh, Descs &ds) const {
 #pragma unroll
         for (int pg = 0; pg < G::PAGES; ++pg) {
             const int32_t page = pid[pg];
@@ -346,11 +355,12 @@ struct DmaPlan {
         }
     }
 
-    // All copies of tile keys [k0, k0 + KT) into the stage at LDS byte address st.
-    __device__ __forceinline__ void issue(const KParams &p, const int32_t *pt, int32_t k0, int32_t lim, int32_t kvh,
-                                          uint32_t st) const {
+    // All copies of tile keys [k0, k0 + KT), pages pid, into the stage at LDS
+    // byte address st.
+    __device__ __forceinline__ void issue_ids(const KParams &p, const int32_t (&pid)[G::PAGES], int32_t k0,
+                                              int32_t lim, int32_t kvh, uint32_t st) const {
         Descs ds;
-        prepare(p, pt, k0, lim, kvh, ds);
+        prepare_ids(p, pid, k0, lim, kvh, ds);
 #pragma unroll
         for (int n = 0; n < PER_TILE; ++n) copy(ds, st, n);
     }
@@ -554,6 +564,21 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
 
     const int32_t *valid_b = VALID ? p.valid + (int64_t)b * p.valid_stride : nullptr;
     const int32_t *bt_b = p.bt ? p.bt + (int64_t)b * p.bt_stride : nullptr;
+    // Block-table window: every wave loads entries [0, WIN_PAGES) of the
+    // sequence's row into registers (entry 64k + lane in win[k]) while the
+    // sequence bounds are read.  The prologue takes its page ids from it by
+    // lane reads -- no dependent load, LDS round trip or barrier before the
+    // first copies -- and it becomes the LDS table the loop starts with.
+    // (Entries past the sequence's keys need no mask: a page's copy size
+    // comes from n_keys.)
+    int32_t win[WIN_PAGES / 64];
+    if constexpr (LD == LD_DMA) {
+#pragma unroll
+        for (int k = 0; k < WIN_PAGES / 64; ++k) {
+            const int32_t pi = lane + k * 64;
+            win[k] = bt_b && pi < p.bt_stride ? bt_b[pi] : -1;
+        }
+    }
 
     // Query fragment: B operand of S^T = K Q^T.  Lane l holds row l%32,
     // dims kk*16 + (l/32)*8 + [0, 8).
@@ -622,15 +647,15 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     float m_run = -INFINITY, l_run = 0.0f;
 
     const int32_t lim = min(nk, p.capacity);  // slots at or past the capacity are zero rows
-    const int32_t p_end = (min(lim, t_hi * G::KT) + 15) / 16;
-    int32_t seg_p0 = t_lo * G::PAGES;
+    // pages this workgroup reads: up to its last tile, within the table row
+    const int32_t p_end = min((min(lim, t_hi * G::KT) + 15) / 16, bt_b ? p.bt_stride : INT32_MAX);
+    // LDS table segment [seg_p0, seg_p0 + seg_len) of page indices (the
+    // register window, when there is one, starts at page 0)
+    const bool windowed = LD == LD_DMA && bt_b != nullptr;
+    int32_t seg_p0 = windowed ? 0 : t_lo * G::PAGES;
+    int32_t seg_len = windowed ? WIN_PAGES : SEG_PAGES;
 
-    // Starts the transfer of tile tt into stage si (a uniform call: every
-    // thread of the workgroup reaches it).  DMA writes the stage directly;
-    // the register paths fill l, which l.store() writes out.  The direct paths
-    // read page ids from the LDS copy of the block table, reloading the next
-    // segment when tt leaves it (every wave is past its last read of the old
-    // one: the previous tile ended with a barrier).
+    // DMA staging: copies straight into a stage (the lane offsets are fixed).
     DmaPlan<D> dma;
     if constexpr (LD == LD_DMA) dma.init();
     const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
@@ -640,26 +665,23 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     // barrier).
     auto seg_index = [&](int32_t tt) {
         int32_t pi = tt * G::PAGES - seg_p0;
-        if (pi + G::PAGES > SEG_PAGES) {
+        if (pi + G::PAGES > seg_len) {
             seg_p0 = tt * G::PAGES;
+            seg_len = SEG_PAGES;
             load_segment(bt_b, seg_p0, p_end, pt);
             __syncthreads();
             pi = 0;
         }
         return pi;
     };
-    // Starts the transfer of tile tt into stage si (a uniform call).  DMA
-    // writes the stage directly; the register paths fill l, which l.store()
-    // writes out.
-    auto issue = [&](RegLoader<D, VALID> &l, int32_t tt, int si) {
+    // Register paths: starts the loads of tile tt into l (a uniform call),
+    // which l.store() writes into a stage.
+    auto issue = [&](RegLoader<D, VALID> &l, int32_t tt) {
         if constexpr (LD == LD_VALID) {
             l.issue_valid(p, valid_b, bt_b, tt * G::KT, nk, kvh);
         } else {
             const int32_t pi = seg_index(tt);
-            if constexpr (LD == LD_DMA)
-                dma.issue(p, pt + pi, tt * G::KT, lim, kvh, smem_lds + si * (G::STAGE * 2));
-            else
-                l.issue_direct(p, pt + pi, tt * G::KT, lim, kvh);
+            l.issue_direct(p, pt + pi, tt * G::KT, lim, kvh);
         }
     };
 
@@ -727,16 +749,38 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     // Prologue: the first NST-1 tiles staged, S of tile t_lo computed.
     RegLoader<D, VALID> ld;
     if constexpr (LD == LD_DMA) {
-        // block table (one round trip), then the query loads and the copies
-        // back to back: the query lands while the copies are being issued
-        if (t_lo < t_hi) load_segment(bt_b, seg_p0, p_end, pt);
-        load_q();
-        if (t_lo < t_hi) {
-            __syncthreads();
-            issue(ld, t_lo, 0);
-            if (t_lo + 1 < t_hi) issue(ld, t_lo + 1, 1);
-            if (t_lo + 2 < t_hi) issue(ld, t_lo + 2, 2);
+        // The first NST-1 tiles' copies go out first, their page ids read
+        // straight from the table (uniform loads, no LDS round trip and no
+        // barrier); then the query loads, which land while the copies stream
+        // in.  The LDS table serves the loop (the barrier below publishes it).
+        static_assert(WIN_PAGES == 128, "two window registers");
+        // (all ids first: each copy is a compiler memory barrier)
+        int32_t pid[NST - 1][G::PAGES];
+#pragma unroll
+        for (int i = 0; i < NST - 1; ++i)
+#pragma unroll
+            for (int pg = 0; pg < G::PAGES; ++pg) {
+                const int32_t pi = (t_lo + i) * G::PAGES + pg;
+                int32_t id = -1;
+                if (pi < p_end) {
+                    id = pi;  // identity table
+                    if (windowed) {
+                        const int32_t w0 = __builtin_amdgcn_readlane(win[0], pi & 63);
+                        const int32_t w1 = __builtin_amdgcn_readlane(win[1], pi & 63);
+                        id = pi < 64 ? w0 : pi < WIN_PAGES ? w1 : __builtin_amdgcn_readfirstlane(bt_b[pi]);
+                    }
+                }
+                pid[i][pg] = id;
+            }
+        if (windowed) {
+            if (wave < WIN_PAGES / 64) pt[wave * 64 + lane] = wave == 0 ? win[0] : win[1];
+        } else if (t_lo < t_hi) {
+            load_segment(bt_b, seg_p0, p_end, pt);
         }
+#pragma unroll
+        for (int i = 0; i < NST - 1; ++i)
+            if (t_lo + i < t_hi) dma.issue_ids(p, pid[i], (t_lo + i) * G::KT, lim, kvh, smem_lds + i * (G::STAGE * 2));
+        load_q();
     } else {
         load_q();
         if (t_lo < t_hi) {
@@ -745,8 +789,8 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                 __syncthreads();
             }
             RegLoader<D, VALID> l1;
-            issue(ld, t_lo, 0);
-            if (t_lo + 1 < t_hi) issue(l1, t_lo + 1, 1);
+            issue(ld, t_lo);
+            if (t_lo + 1 < t_hi) issue(l1, t_lo + 1);
             ld.store(smem);
             if (t_lo + 1 < t_hi) l1.store(smem + G::STAGE);
         }
@@ -800,7 +844,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             else
                 dma.empty(dsc);
         } else {
-            if (more) issue(ld, t + NST - 1, nxl);
+            if (more) issue(ld, t + NST - 1);
         }
 
         if (wave_live) {
@@ -900,25 +944,40 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
         l_run = a + c;
     }
 
-    // Output rows: the normalised O (f32) or, with splits, the unnormalised
-    // partial with its (m, l).  Lane l holds dims dt*32 + j*8 + (l/32)*4 + [0,4)
-    // of row l%32, so a direct 16-byte store touches 64 rows (cache lines) per
-    // instruction.  Where the stages have room, each wave instead writes its 32
-    // rows x D block into LDS (16-byte chunk c of row r at chunk c ^ (r & 31),
-    // which spreads the 32 rows of one write over the banks) and stores whole
-    // rows: D*4 contiguous bytes per row, 1024/D rows an instruction.
-    const bool partial = p.splits > 1;
-    const int64_t unit_row0 =
-        partial ? ((int64_t)(b * p.hkv + kvh) * p.splits + split) * ((int64_t)p.row_tiles * ROWS_PER_WG) : 0;
-    if (partial && row_ok && lhi == 0) {
-        const int64_t rowi = unit_row0 + my_row;
-        p.ws_ml[rowi * 2] = m_run == -INFINITY ? -INFINITY : m_run * p.c_log2;
-        p.ws_ml[rowi * 2 + 1] = l_run;
-    }
-    // (a split's partial is normalised too, and stored in f16: O/l of a split
-    // is a weighted mean of V rows, so f16 keeps 11 bits relative to each
-    // element; the merge reweights the splits by l)
     const float sc = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    // Split partials: O / l in f16 (O/l of a split is a weighted mean of V
+    // rows, so f16 keeps 11 bits relative to each element; the merge
+    // reweights the splits by l) with (m, l) per row.  Only the merge kernel
+    // reads them, so each wave stores its 32-row block in the accumulator
+    // order: every store instruction writes 512 contiguous bytes, with no
+    // staging through LDS.  (Rows past the end carry values nothing reads.)
+    if (p.splits > 1) {
+        const int64_t unit_row0 = ((int64_t)(b * p.hkv + kvh) * p.splits + split) * ((int64_t)p.row_tiles * ROWS_PER_WG);
+        if (row_ok && lhi == 0) {
+            const int64_t rowi = unit_row0 + my_row;
+            *reinterpret_cast<float2 *>(p.ws_ml + rowi * 2) =
+                float2{m_run == -INFINITY ? -INFINITY : m_run * p.c_log2, l_run};
+        }
+        if (wave_live) {
+            uint16_t *blk = p.ws_o + (unit_row0 + row0 + wave * ROWS_PER_WAVE) * D + lane * 4;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
+                                     acc_o[dt][j * 4 + 3] * sc};
+                    *reinterpret_cast<u32x2 *>(blk + (dt * 4 + j) * 256) = f16x4_bits(v);
+                }
+        }
+        return;
+    }
+    // Output rows, the normalised O (f32).  Lane l holds dims dt*32 + j*8 +
+    // (l/32)*4 + [0,4) of row l%32, so a direct 16-byte store touches 64 rows
+    // (cache lines) per instruction.  Where the stages have room, each wave
+    // instead writes its 32 rows x D block into LDS (16-byte chunk c of row r
+    // at chunk c ^ (r & 31), which spreads the 32 rows of one write over the
+    // banks) and stores whole rows: D*4 contiguous bytes per row, 1024/D rows
+    // an instruction.
     constexpr int CHR = D / 4;  // 16-byte chunks in a row of D floats
     if constexpr (NST * G::STAGE * 2 >= WAVES * ROWS_PER_WAVE * D * 4) {
         // every wave is past its last stage read (the loop ended with a barrier)
@@ -947,9 +1006,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
         // wave, -1 past the last row; a store takes its rows' offsets by lane
         // reads (scalar when one row fills the instruction)
         int64_t dst_off = -1;
-        if (row_ok)
-            dst_off = partial ? (unit_row0 + my_row) * D
-                              : (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
+        if (row_ok) dst_off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
         const uint32_t off_lo = (uint32_t)dst_off, off_hi = (uint32_t)((uint64_t)dst_off >> 32);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -968,78 +1025,76 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                 for (int u = 1; u < RPI; ++u) off = sub == u ? cand[u] : off;
             }
             if (off < 0) continue;
-            if (partial)
-                *reinterpret_cast<u32x2 *>(p.ws_o + off + c * 4) = f16x4_bits(rv[i]);
-            else
-                *reinterpret_cast<f32x4 *>(p.out + off + c * 4) = rv[i];
+            *reinterpret_cast<f32x4 *>(p.out + off + c * 4) = rv[i];
         }
     } else {
         if (!row_ok) return;
-        const int64_t off = partial ? (unit_row0 + my_row) * D
-                                    : (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
+        const int64_t off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
                                  acc_o[dt][j * 4 + 3] * sc};
-                const int64_t e = off + dt * 32 + j * 8 + lhi * 4;
-                if (partial)
-                    *reinterpret_cast<u32x2 *>(p.ws_o + e) = f16x4_bits(v);
-                else
-                    *reinterpret_cast<f32x4 *>(p.out + e) = v;
+                *reinterpret_cast<f32x4 *>(p.out + off + dt * 32 + j * 8 + lhi * 4) = v;
             }
     }
 }
 
 // Combines split partials (m in log2 units, O_s already divided by l_s):
-// m = max m_s, w_s = l_s 2^(m_s - m), out = sum w_s O_s / sum w_s.  One thread
-// per (row, 8 dims); the loads of up to MS splits are all issued before any is
-// used (a loop over splits would wait out one memory round trip per split).
+// m = max m_s, w_s = l_s 2^(m_s - m), out = sum w_s O_s / sum w_s.  A wave
+// takes one 8-dim chunk of a 32-row block, lane l the four dims that lane l of
+// the producing wave stored (row l%32, dims chunk*8 + (l/32)*4 + [0,4)), so
+// each split's partial arrives as one contiguous 512-byte read.  The loads of
+// up to MS splits are all issued before any is used.
 template <int D, int MS>
 __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
-    const int64_t rows_per_unit = (int64_t)p.row_tiles * ROWS_PER_WG;
-    const int64_t total = (int64_t)p.batch * p.hkv * rows_per_unit * (D / 8);
+    constexpr int NC = D / 8;
+    const int32_t blocks_per_unit = p.row_tiles * (ROWS_PER_WG / 32);
+    const int64_t total = (int64_t)p.batch * p.hkv * blocks_per_unit * NC * 64;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * blockDim.x) {
-        const int d8 = (int)(idx % (D / 8));
-        int64_t r = idx / (D / 8);
-        const int32_t row = (int32_t)(r % rows_per_unit);
-        r /= rows_per_unit;
-        const int kvh = (int)(r % p.hkv);
-        const int b = (int)(r / p.hkv);
+        const int lane = (int)(idx & 63);
+        int64_t w = idx >> 6;
+        const int c = (int)(w % NC);
+        w /= NC;
+        const int32_t blk = (int32_t)(w % blocks_per_unit);
+        w /= blocks_per_unit;
+        const int kvh = (int)(w % p.hkv);
+        const int b = (int)(w / p.hkv);
+        const int32_t row = blk * 32 + (lane & 31);
         const int32_t q_begin = p.cu_q ? p.cu_q[b] : 0;
         const int32_t nq = p.cu_q ? p.cu_q[b + 1] - q_begin : p.nq_single;
         if (row >= nq * p.G) continue;
+        const int64_t rows_per_unit = (int64_t)blocks_per_unit * 32;
         const int64_t unit0 = (int64_t)(b * p.hkv + kvh) * p.splits;
         float ms[MS], ls[MS];
-        u32x4 os[MS];
+        u32x2 os[MS];
 #pragma unroll
         for (int s = 0; s < MS; ++s) {
-            const int64_t ri = (unit0 + (s < p.splits ? s : 0)) * rows_per_unit + row;
-            const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + ri * 2);
+            const int64_t u = (unit0 + (s < p.splits ? s : 0)) * rows_per_unit;
+            const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + (u + row) * 2);
             ms[s] = s < p.splits ? ml.x : -INFINITY;
             ls[s] = ml.y;
-            os[s] = *reinterpret_cast<const u32x4 *>(p.ws_o + ri * D + d8 * 8);
+            os[s] = *reinterpret_cast<const u32x2 *>(p.ws_o + (u + blk * 32) * D + (c * 64 + lane) * 4);
         }
         float m = -INFINITY;
 #pragma unroll
         for (int s = 0; s < MS; ++s) m = fmaxf(m, ms[s]);
-        float l = 0.0f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float l = 0.0f, o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < MS; ++s) {
-            const float w = ms[s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[s] - m) * ls[s];
-            l += w;
+            const float wgt = ms[s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[s] - m) * ls[s];
+            l += wgt;
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                o[e] += w * (float)__builtin_bit_cast(_Float16, (uint16_t)(os[s][e >> 1] >> ((e & 1) * 16)));
+            for (int e = 0; e < 4; ++e)
+                o[e] += wgt * (float)__builtin_bit_cast(_Float16, (uint16_t)(os[s][e >> 1] >> ((e & 1) * 16)));
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         const int32_t tok = row / p.G;
         const int32_t head = kvh * p.G + row % p.G;
-        float *dst = p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + d8 * 8;
+        float *dst = p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + c * 8 + (lane >> 5) * 4;
         *reinterpret_cast<f32x4 *>(dst) = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
-        *reinterpret_cast<f32x4 *>(dst + 4) = f32x4{o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv};
     }
 }
 
@@ -1077,7 +1132,7 @@ hipError_t dispatch_mask(const KParams &kp, int mask, int ld, bool qf32, hipStre
 
 template <int D>
 hipError_t launch_merge(const KParams &kp, hipStream_t stream) {
-    const int64_t total = (int64_t)kp.batch * kp.hkv * kp.row_tiles * ROWS_PER_WG * (D / 8);
+    const int64_t total = (int64_t)kp.batch * kp.hkv * kp.row_tiles * ROWS_PER_WG * (D / 4);
     int64_t g = (total + 255) / 256;
     if (g > 65536) g = 65536;
     if (kp.splits <= 4)

@@ -176,7 +176,8 @@ typedef struct emb_attn_args {
      * valid-slot list), tiles are copied into LDS without conversion */
     const void *k_pool, *v_pool;
     const void *v16_pool;
-    const int32_t *block_tables; /* device [batch][bt_stride] or NULL (identity) */
+    const int32_t *block_tables; /* device [batch][bt_stride] or NULL (identity); keys
+                                    past bt_stride*16 read as zero rows */
     int32_t bt_stride;
     const int32_t *valid_slots;  /* device [batch][valid_stride] or NULL: key j is
                                     logical slot j; else key j is slot valid[j]
