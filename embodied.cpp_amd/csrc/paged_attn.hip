@@ -890,6 +890,10 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
                         l_run = __builtin_amdgcn_fdot2(f16x2{pf[eb][r >> 3][(r & 7) - 1], pf[eb][r >> 3][r & 7]},
                                                        f16x2{(_Float16)1.0f, (_Float16)1.0f}, l_run, false);
                 }
+                // keep this step's softmax here: without a use, IR passes sink
+                // the whole softmax below the S MFMAs (sched_barrier only binds
+                // the machine scheduler)
+                asm volatile("" : "+v"(l_run));
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (t + 1 < t_hi) apply_mask(s_nxt, (t + 1) * G::KT);
