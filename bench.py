@@ -229,9 +229,15 @@ def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
             lp.attend(0, st, scale)
     ms_layer, _ = c.time_graph(per_layer, max(2, steps // 2), 2)
 
+    # cold vs warm: eager steps, each after 1 GiB is rewritten on the stream
+    # (flushes the 256 MB MALL and the L2s; outside the timed region) or not
+    cold_us, warm_us = cold_warm_steps(c, one_step, n=max(5, steps // 4))
+
     ab = P.attn_bytes()
     return dict(
         us_per_step=ms_step * 1e3,
+        us_per_step_cold=cold_us,
+        us_per_step_warm_eager=warm_us,
         us_per_step_10step_graph=ms_ten * 1e3 / 10,
         us_per_step_dependent_layers=ms_layer * 1e3,
         attn_us_single_launch=attn_us,
@@ -242,6 +248,31 @@ def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
         attn_flops_per_launch=P.attn_flops(),
         survey_bytes_per_step=P.survey_step_bytes(),
     )
+
+
+def cold_warm_steps(c: Ctx, fn, n):
+    """Median GPU time (us) of fn(stream) run eagerly: cold = right after 1 GiB
+    is written on the stream (flushes the 256 MB MALL and the L2s; the write
+    also gives the host time to enqueue the step), warm = the second of two
+    back-to-back runs."""
+    torch = c.torch
+    flush = torch.empty(1 << 28, dtype=torch.float32, device=c.dev)
+    Ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    cold, warm = [], []
+    for _ in range(n):
+        e0, e1, e2 = Ev(), Ev(), Ev()
+        with torch.cuda.stream(c.stream):
+            flush.fill_(1.0)
+            e0.record(c.stream)
+            fn(c.stream)
+            e1.record(c.stream)
+            fn(c.stream)
+            e2.record(c.stream)
+        torch.cuda.synchronize()
+        cold.append(e0.elapsed_time(e1) * 1e3)
+        warm.append(e1.elapsed_time(e2) * 1e3)
+    del flush
+    return float(np.median(cold)), float(np.median(warm))
 
 
 def bench_cfg4(c: Ctx, steps, warmup):
@@ -595,7 +626,7 @@ def main():
     ap.add_argument("--configs", default="cfg1,cfg2,cfg3,cfg4,cfg5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="profiling targets: cfg1_attn (the headline kernel loop), cfg3_attn, cfg5_gemm, "
+                    help="profiling targets: cfg1_attn (the headline kernel loop), cfg2_attn, cfg3_attn, cfg4_attn, cfg5_gemm, "
                          "copy_calib (a plain 256 MiB device copy, the PMC byte-counter calibration)")
     ap.add_argument("--traffic-summary", default="", metavar="DIR",
                     help="write profiles/" + TRAFFIC_FILE + " from the four rocprofv3 --pmc runs under DIR "
@@ -624,6 +655,24 @@ def main():
         P.set_splits(int(os.environ.get("EMB_SPLITS", "3")))
         for i in range(args.warmup + args.steps):
             P.attend(i, c.stream, 1 / 16)
+        c.torch.cuda.synchronize()
+        log("profile loop done")
+        return
+    if args.only == "cfg2_attn":  # prefill attention, 18 layers, split 1
+        P = PagedLayers(c, 0xE3BD0001, [0] * 18, 816, 8, 1, 256, n_steps=1)
+        P.set_splits(1)
+        for _ in range(args.warmup + args.steps):
+            P.attend(0, c.stream, 1 / 16)
+        c.torch.cuda.synchronize()
+        log("profile loop done")
+        return
+    if args.only == "cfg4_attn":  # B = 64 sessions, one layer, split 1
+        g = MT64(0xE3BD0004)
+        lens = [300 + g.next() % 901 for _ in range(64)]
+        P = PagedLayers(c, 0xE3BD0004 + 64, lens, 51, 8, 1, 256, n_steps=2)
+        P.set_splits(1)
+        for _ in range(args.warmup + args.steps):
+            P.attend(0, c.stream, 1 / 16)
         c.torch.cuda.synchronize()
         log("profile loop done")
         return
