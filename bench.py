@@ -136,6 +136,8 @@ class PagedLayers:
         self.vnew = [c.synth(seed + 200 + s, self.L * n_new * hkv * d) for s in range(n_steps)]
         self.cu_q = c.i32(np.arange(self.L + 1) * n_new)
         self.nk = c.i32(self.n_keys)
+        # equal caches launch in the uniform form (no bounds arrays to read)
+        self.uniform = len(set(self.n_keys)) == 1
         self.out = torch.zeros((self.L * n_new, hq, d), dtype=torch.float32, device=c.dev)
         self.ws = None
         torch.cuda.synchronize()
@@ -157,7 +159,10 @@ class PagedLayers:
         self.c.emb.paged_attention(q=self.q[s], out=self.out, k_pool=self.k_pool, v_pool=self.v_pool,
                                    v16_pool=self.v16_pool,
                                    batch=self.L, hq=self.hq, hkv=self.hkv, d=self.d, max_q=self.n_new,
-                                   scale=scale, capacity=self.cap, cu_q=self.cu_q, n_keys=self.nk,
+                                   scale=scale, capacity=self.cap,
+                                   cu_q=None if self.uniform else self.cu_q,
+                                   n_keys=None if self.uniform else self.nk,
+                                   n_keys_uniform=self.n_keys[0] if self.uniform else 0,
                                    block_tables=self.bt, bt_stride=self.bt_stride, splits=self.splits,
                                    workspace=self.ws, stream=stream)
 
@@ -359,8 +364,6 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
         emb.kv_append(base_k, base_v, H * d, cap, c.i32(np.arange(cap)), bt_d, cap, kp, vp, H, d, v16_pool=v16)
         pools.append((kp, vp, v16, bt_d))
     out = torch.empty((C, H, d), dtype=torch.float32, device=c.dev)
-    cu = c.i32([0, C])
-    nk = c.i32([cap])
     # the slot range the evicted oldest chunk held (chunk 0), reused by the new chunk
     new_slots = c.i32(np.arange(C))
     scale = 1 / math.sqrt(d)
@@ -378,7 +381,7 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
         if append:
             emb.kv_append(knew, vnew, H * d, C, new_slots, bt, cap, kp, vp, H, d, stream=st, v16_pool=v16)
         emb.paged_attention(q=q, out=out, k_pool=kp, v_pool=vp, v16_pool=v16, batch=1, hq=H, hkv=H, d=d, max_q=C,
-                            scale=scale, capacity=cap, cu_q=cu, n_keys=nk, block_tables=bt, bt_stride=pages,
+                            scale=scale, capacity=cap, n_keys_uniform=cap, block_tables=bt, bt_stride=pages,
                             splits=cur_split[0], workspace=cur_split[1], stream=st)
 
     if eager_only:  # profiling: plain launches of the attention kernel
@@ -451,7 +454,6 @@ def bench_cfg5(c: Ctx, steps, warmup):
     qo = torch.empty((M, H * d), dtype=torch.int16, device=c.dev)
     slots = c.i32(np.arange(C))  # the new chunk takes the slots of the evicted oldest chunk
     out = torch.empty((C, H, d), dtype=torch.float32, device=c.dev)
-    cu, nk = c.i32([0, C]), c.i32([cap])
 
     def fused(st):
         emb.w8a16_qkv_append(x, qw, sc, M, K, H * d, qo, slots, bt, cap, kp, vp, H, d, stream=st, v16_pool=v16)
@@ -462,7 +464,7 @@ def bench_cfg5(c: Ctx, steps, warmup):
     def step(st):
         fused(st)
         emb.paged_attention(q=qo, out=out, k_pool=kp, v_pool=vp, v16_pool=v16, batch=1, hq=H, hkv=H, d=d, max_q=C,
-                            scale=1 / math.sqrt(d), capacity=cap, cu_q=cu, n_keys=nk, block_tables=bt,
+                            scale=1 / math.sqrt(d), capacity=cap, n_keys_uniform=cap, block_tables=bt,
                             bt_stride=pages, splits=att_splits, workspace=ws, stream=st)
     ms_f, _ = c.time_graph(fused, steps, warmup)
     ms_s, _ = c.time_graph(step, max(2, steps // 4), 2)

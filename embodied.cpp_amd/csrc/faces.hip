@@ -99,15 +99,11 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(StageGeom g, uint16_t *__
     }
 }
 
-// Query offsets and key counts of the sequences, and the block tables of
-// `batch` sequences that share one staged K/V set (kv_batch == 1: every table
-// is the identity over pages [0, pps)).
-__global__ void tables_kernel(int32_t *__restrict__ bt, int32_t pps, int32_t batch, int32_t kv_batch,
-                              int32_t *__restrict__ cu_q, int32_t n_q, int32_t *__restrict__ nk, int32_t n_kv) {
+// The block tables of `batch` sequences that share one staged K/V set
+// (kv_batch == 1: every table is the identity over pages [0, pps)).
+__global__ void tables_kernel(int32_t *__restrict__ bt, int32_t pps, int32_t batch) {
     const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < batch * pps && kv_batch == 1) bt[i] = i % pps;
-    if (i <= batch) cu_q[i] = i * n_q;
-    if (i < batch) nk[i] = n_kv;
+    if (i < batch * pps) bt[i] = i % pps;
 }
 
 // Queries to bf16 [batch][n_q][heads][dp], dims past d_src zero.
@@ -195,7 +191,7 @@ struct Plan {
     int32_t mask_batch;  // 0 = no f32 mask staging
     int64_t q_blocks, k_blocks;  // flex block map (0 = none)
     // byte offsets into the workspace
-    size_t off_k, off_v, off_v16, off_bt, off_cu, off_nk, off_q, off_mask, off_bmap, off_out, total;
+    size_t off_k, off_v, off_v16, off_bt, off_q, off_mask, off_bmap, off_out, total;
 
     void layout() {
         const size_t pool = (size_t)kv_batch * pps * hkv * 16 * dp * 2;
@@ -208,10 +204,6 @@ struct Plan {
         o += up256(pool);
         off_bt = o;
         o += up256((size_t)batch * pps * 4);
-        off_cu = o;
-        o += up256((size_t)(batch + 1) * 4);
-        off_nk = o;
-        o += up256((size_t)batch * 4);
         off_q = o;
         if (stage_q) o += up256((size_t)batch * n_q * hq * dp * 2);
         off_mask = o;
@@ -231,17 +223,18 @@ int stage_kv(const Plan &pl, const Src4 &k, const Src4 &v, char *ws, hipStream_t
                        (uint16_t *)(ws + pl.off_v), (uint16_t *)(ws + pl.off_v16), (int32_t *)(ws + pl.off_bt));
     int rc = launch_check("stage_kv");
     if (rc) return rc;
-    const int32_t n = std::max(pl.batch * pl.pps, pl.batch + 1);
+    if (pl.kv_batch != 1) return EMB_OK;  // stage_kv_kernel wrote one table per sequence
+    const int32_t n = pl.batch * pl.pps;
     hipLaunchKernelGGL(tables_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, (int32_t *)(ws + pl.off_bt), pl.pps,
-                       pl.batch, pl.kv_batch, (int32_t *)(ws + pl.off_cu), pl.n_q, (int32_t *)(ws + pl.off_nk),
-                       pl.n_kv);
+                       pl.batch);
     return launch_check("tables");
 }
 
 void base_args(const Plan &pl, char *ws, float scale, emb_attn_args &a) {
     a = emb_attn_args{};
-    a.cu_q = (const int32_t *)(ws + pl.off_cu);
-    a.n_keys = (const int32_t *)(ws + pl.off_nk);
+    // every sequence has n_q queries and n_kv keys: the uniform form, which the
+    // kernels read no bounds arrays for
+    a.n_keys_uniform = pl.n_kv;
     a.k_pool = ws + pl.off_k;
     a.v_pool = ws + pl.off_v;
     a.v16_pool = ws + pl.off_v16;

@@ -118,7 +118,7 @@ struct KParams {
     const int32_t *cu_q;
     const int32_t *n_keys;
     const int32_t *q_pos0;
-    int32_t nq_single, nk_single;  // used when cu_q / n_keys are null (batch 1)
+    int32_t nq_single, nk_single;  // per-sequence bounds when cu_q / n_keys are null
     const uint16_t *k_pool;
     const uint16_t *v_pool;
     const uint16_t *v16_pool;
@@ -542,7 +542,9 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     const int kvh = rest % p.hkv;
     const int b = rest / p.hkv;
 
-    const int32_t q_begin = p.cu_q ? p.cu_q[b] : 0;
+    // bounds of sequence b (without cu_q / n_keys every sequence has nq_single
+    // queries and nk_single keys, known before any load)
+    const int32_t q_begin = p.cu_q ? p.cu_q[b] : b * p.nq_single;
     const int32_t nq = p.cu_q ? p.cu_q[b + 1] - q_begin : p.nq_single;
     const int32_t nk = p.n_keys ? p.n_keys[b] : p.nk_single;
     const int32_t rows = nq * p.G;
@@ -828,8 +830,16 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
     constexpr int NPV = G::KB * 2 * (D / 32);  // P.V MFMAs a tile
     constexpr int EPM = G::KB * 16 / NS;       // score elements per step (both phases)
     static_assert(NPV * EPM == G::KB * 16 && 2 * DmaPlan<D>::PER_TILE <= NPV, "tile schedule");
-    int cur = 0;
-    for (int32_t t = t_lo; t < t_hi; ++t) {
+    //
+    // The loop runs NST tiles an iteration (tile t_lo + i sits in stage i %
+    // NST), so every stage index is a compile-time constant: LDS addresses
+    // take the stage as an immediate offset, and the scores of consecutive
+    // tiles alternate between two register sets instead of being copied.
+    for (int32_t t0 = t_lo; t0 < t_hi; t0 += NST) {
+#pragma unroll
+      for (int cur = 0; cur < NST; ++cur) {
+        const int32_t t = t0 + cur;
+        if (t >= t_hi) break;
         const int nx1 = cur + 1 == NST ? 0 : cur + 1;
         const int nxl = cur == 0 ? NST - 1 : cur - 1;  // receives tile t + NST - 1
         const bool more = t + NST - 1 < t_hi;
@@ -940,7 +950,7 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             ld.store(smem + nxl * G::STAGE);
         }
         __syncthreads();
-        cur = nx1;
+      }
     }
     {
         float a, c;
@@ -1067,7 +1077,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
         const int kvh = (int)(w % p.hkv);
         const int b = (int)(w / p.hkv);
         const int32_t row = blk * 32 + (lane & 31);
-        const int32_t q_begin = p.cu_q ? p.cu_q[b] : 0;
+        const int32_t q_begin = p.cu_q ? p.cu_q[b] : b * p.nq_single;
         const int32_t nq = p.cu_q ? p.cu_q[b + 1] - q_begin : p.nq_single;
         if (row >= nq * p.G) continue;
         const int64_t rows_per_unit = (int64_t)blocks_per_unit * 32;
@@ -1158,8 +1168,13 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     EMB_CHECK_ARG(a->batch > 0 && a->hq > 0 && a->hkv > 0 && a->hq % a->hkv == 0, "bad head counts");
     EMB_CHECK_ARG(a->head_dim == 64 || a->head_dim == 128 || a->head_dim == 256, "head_dim must be 64, 128 or 256");
     EMB_CHECK_ARG(a->max_q > 0, "max_q must be positive");
-    EMB_CHECK_ARG((a->cu_q && a->n_keys) || (!a->cu_q && !a->n_keys && a->batch == 1),
-                  "cu_q and n_keys are required for batch > 1");
+    EMB_CHECK_ARG((a->cu_q != nullptr) == (a->n_keys != nullptr), "cu_q and n_keys go together");
+    if (!a->cu_q && nk_single == 0) {
+        // uniform batch: max_q queries and n_keys_uniform keys per sequence
+        EMB_CHECK_ARG(a->n_keys_uniform > 0, "n_keys_uniform must be positive when cu_q and n_keys are NULL");
+        nq_single = a->max_q;
+        nk_single = a->n_keys_uniform;
+    }
     EMB_CHECK_ARG(a->capacity > 0, "capacity must be positive");
     EMB_CHECK_ARG(!a->valid_slots || a->valid_stride >= 0, "bad valid_stride");
     EMB_CHECK_ARG(!a->block_tables || a->bt_stride > 0, "bad bt_stride");

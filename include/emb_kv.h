@@ -168,6 +168,9 @@ typedef struct emb_attn_args {
     /* output f32 [total_q][hq][d], token stride out_stride elements */
     float *out;
     int64_t out_stride;
+    /* cu_q and n_keys are both given, or both NULL: then every sequence has
+     * max_q query tokens (sequence b owns tokens b*max_q..) and
+     * n_keys_uniform keys, and the kernels read no per-sequence bounds */
     const int32_t *cu_q;       /* device [batch+1] */
     const int32_t *n_keys;     /* device [batch]: keys per sequence */
     const int32_t *q_pos0;     /* device [batch] or NULL: position of query 0 in
@@ -201,6 +204,7 @@ typedef struct emb_attn_args {
      * emb_attn_workspace_bytes(...) bytes of device memory. */
     int32_t splits;
     void *workspace;
+    int32_t n_keys_uniform;            /* keys per sequence when cu_q and n_keys are NULL */
 } emb_attn_args;
 
 size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_t hkv,

@@ -64,10 +64,13 @@ class Seqs:
                              hkv, d, self.cap, self.kp, self.vp)
         self.cu_q = np.concatenate([[0], np.cumsum(n_q)]).astype(np.int32)
 
-    def run(self, emb, torch, dev, scale, splits=1, **kw):
+    def run(self, emb, torch, dev, scale, splits=1, uniform=False, **kw):
         """Runs the attention twice -- tiles staged through registers from the bf16
         V pool, and copied into LDS from the f16 V shadow -- and requires the two
-        to agree bit for bit (same arithmetic, same conversions)."""
+        to agree bit for bit (same arithmetic, same conversions).  uniform: the
+        batch goes in the form without bounds arrays (equal sequences only)."""
+        if uniform:
+            assert len(set(self.n_keys)) == 1 and len(set(self.n_q)) == 1
         ws = None
         if splits > 1:
             nb = emb.attn_workspace_bytes(len(self.n_q), max(self.n_q), self.hq, self.hkv, self.d, splits)
@@ -81,7 +84,9 @@ class Seqs:
             out = torch.full((int(self.cu_q[-1]), self.hq, self.d), float("nan"), dtype=torch.float32, device=dev)
             emb.paged_attention(q=keep["q"], out=out, k_pool=keep["kp"], v_pool=keep["vp"], v16_pool=v16,
                                 batch=len(self.n_q), hq=self.hq, hkv=self.hkv, d=self.d, max_q=max(self.n_q),
-                                scale=scale, capacity=self.cap, cu_q=keep["cu"], n_keys=keep["nk"],
+                                scale=scale, capacity=self.cap, cu_q=None if uniform else keep["cu"],
+                                n_keys=None if uniform else keep["nk"],
+                                n_keys_uniform=self.n_keys[0] if uniform else 0,
                                 block_tables=keep["bt"], bt_stride=self.bt_stride, splits=splits, workspace=ws,
                                 **kw)
             torch.cuda.synchronize()
@@ -107,6 +112,20 @@ def test_pi05_action_expert_shape(emb, orc, torch_dev):
     assert_close(got4, s.oracle(orc, 0, scale), "pi05 cfg1 split-K 4")
     got6 = s.run(emb, torch, dev, scale, splits=6)[0]
     assert_close(got6, s.oracle(orc, 0, scale), "pi05 cfg1 split-K 6")
+
+
+def test_uniform_batch_form(emb, orc, torch_dev):
+    """cfg1 layers batched in one launch without bounds arrays (every sequence 51 queries
+    over 867 keys): bit-identical to the launch with cu_q / n_keys, and within the bar."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0010)
+    s = Seqs(orc, rng, [867] * 3, [51] * 3, 8, 1, 256)
+    for splits in (1, 3):
+        arr = s.run(emb, torch, dev, 1 / 16, splits=splits)
+        uni = s.run(emb, torch, dev, 1 / 16, splits=splits, uniform=True)
+        for b in range(3):
+            assert np.array_equal(arr[b], uni[b]), f"uniform form differs, splits {splits} seq {b}"
+            assert_close(uni[b], s.oracle(orc, b, 1 / 16), f"uniform seq {b} splits {splits}")
 
 
 def test_multi_session_sweep(emb, orc, torch_dev):

@@ -169,9 +169,12 @@ def test_device_entry_points_reject_bad_arguments(emb):
     with pytest.raises(RuntimeError, match="cu_q"):
         emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=2, hq=8, hkv=1, d=128,
                             max_q=4, scale=0.1, capacity=64)
+    with pytest.raises(RuntimeError, match="go together"):
+        emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=2, hq=8, hkv=1, d=128,
+                            max_q=4, scale=0.1, capacity=64, cu_q=256)
     with pytest.raises(RuntimeError, match="workspace"):
         emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=1, hq=8, hkv=1, d=128,
-                            max_q=4, scale=0.1, capacity=64, splits=4)
+                            max_q=4, scale=0.1, capacity=64, splits=4, n_keys_uniform=40)
     assert L.lingbot_runtime_kv_attn_f32(None, None, None, None, None, 1, 1, 1, 64, 0.1, None) == -1
     # f16 partial rows (O/l) plus f32 (m, l) per row
     assert emb.attn_workspace_bytes(1, 51, 8, 1, 256, 4) == 4 * 512 * (256 * 2 + 2 * 4)
