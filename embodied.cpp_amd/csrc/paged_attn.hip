@@ -1057,21 +1057,25 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
 
 // Combines split partials (m in log2 units, O_s already divided by l_s):
 // m = max m_s, w_s = l_s 2^(m_s - m), out = sum w_s O_s / sum w_s.  A wave
-// takes one 8-dim chunk of a 32-row block, lane l the four dims that lane l of
-// the producing wave stored (row l%32, dims chunk*8 + (l/32)*4 + [0,4)), so
-// each split's partial arrives as one contiguous 512-byte read.  The loads of
-// up to MS splits are all issued before any is used.
-template <int D, int MS>
+// takes NCH 8-dim chunks of a 32-row block, lane l of chunk c the four dims
+// that lane l of the producing wave stored there (row l%32, dims c*8 +
+// (l/32)*4 + [0,4)), so each split's partial of a chunk arrives as one
+// contiguous 512-byte read.  Every load of the wave (all splits, all its
+// chunks) is issued before any is used, and the grid is small enough that
+// every wave is resident at once: the kernel costs about one memory latency.
+template <int D, int MS, int NCH>
 __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
-    constexpr int NC = D / 8;
+    constexpr int NC = D / 8;      // 8-dim chunks of a row
+    constexpr int NG = NC / NCH;   // chunk groups, one wave each
+    static_assert(NC % NCH == 0, "chunk groups");
     const int32_t blocks_per_unit = p.row_tiles * (ROWS_PER_WG / 32);
-    const int64_t total = (int64_t)p.batch * p.hkv * blocks_per_unit * NC * 64;
+    const int64_t total = (int64_t)p.batch * p.hkv * blocks_per_unit * NG * 64;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * blockDim.x) {
         const int lane = (int)(idx & 63);
         int64_t w = idx >> 6;
-        const int c = (int)(w % NC);
-        w /= NC;
+        const int cg = (int)(w % NG);
+        w /= NG;
         const int32_t blk = (int32_t)(w % blocks_per_unit);
         w /= blocks_per_unit;
         const int kvh = (int)(w % p.hkv);
@@ -1083,32 +1087,46 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
         const int64_t rows_per_unit = (int64_t)blocks_per_unit * 32;
         const int64_t unit0 = (int64_t)(b * p.hkv + kvh) * p.splits;
         float ms[MS], ls[MS];
-        u32x2 os[MS];
+        u32x2 os[MS][NCH];
 #pragma unroll
         for (int s = 0; s < MS; ++s) {
-            const int64_t u = (unit0 + (s < p.splits ? s : 0)) * rows_per_unit;
-            const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + (u + row) * 2);
-            ms[s] = s < p.splits ? ml.x : -INFINITY;
-            ls[s] = ml.y;
-            os[s] = *reinterpret_cast<const u32x2 *>(p.ws_o + (u + blk * 32) * D + (c * 64 + lane) * 4);
+            ms[s] = -INFINITY;
+            ls[s] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NCH; ++j) os[s][j] = u32x2{0u, 0u};
+            if (s < p.splits) {
+                const int64_t u = (unit0 + s) * rows_per_unit;
+                const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + (u + row) * 2);
+                ms[s] = ml.x;
+                ls[s] = ml.y;
+                const uint16_t *src = p.ws_o + (u + blk * 32) * D + (cg * NCH * 64 + lane) * 4;
+#pragma unroll
+                for (int j = 0; j < NCH; ++j) os[s][j] = *reinterpret_cast<const u32x2 *>(src + j * 256);
+            }
         }
         float m = -INFINITY;
 #pragma unroll
         for (int s = 0; s < MS; ++s) m = fmaxf(m, ms[s]);
-        float l = 0.0f, o[4] = {0.f, 0.f, 0.f, 0.f};
+        float wgt[MS], l = 0.0f;
 #pragma unroll
         for (int s = 0; s < MS; ++s) {
-            const float wgt = ms[s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[s] - m) * ls[s];
-            l += wgt;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                o[e] += wgt * (float)__builtin_bit_cast(_Float16, (uint16_t)(os[s][e >> 1] >> ((e & 1) * 16)));
+            wgt[s] = ms[s] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[s] - m) * ls[s];
+            l += wgt[s];
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         const int32_t tok = row / p.G;
         const int32_t head = kvh * p.G + row % p.G;
-        float *dst = p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + c * 8 + (lane >> 5) * 4;
-        *reinterpret_cast<f32x4 *>(dst) = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+        float *dst = p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + cg * NCH * 8 + (lane >> 5) * 4;
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+            float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < MS; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    o[e] += wgt[s] * (float)__builtin_bit_cast(_Float16, (uint16_t)(os[s][j][e >> 1] >> ((e & 1) * 16)));
+            *reinterpret_cast<f32x4 *>(dst + j * 8) = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+        }
     }
 }
 
@@ -1146,17 +1164,20 @@ hipError_t dispatch_mask(const KParams &kp, int mask, int ld, bool qf32, hipStre
 
 template <int D>
 hipError_t launch_merge(const KParams &kp, hipStream_t stream) {
-    const int64_t total = (int64_t)kp.batch * kp.hkv * kp.row_tiles * ROWS_PER_WG * (D / 4);
-    int64_t g = (total + 255) / 256;
-    if (g > 65536) g = 65536;
+    // four chunks a wave up to 8 splits, fewer past that (registers)
+    const int64_t rows = (int64_t)kp.batch * kp.hkv * kp.row_tiles * ROWS_PER_WG;
+    auto grid = [&](int nch) {
+        const int64_t g = (rows * (D / 8) / nch * 2 + 255) / 256;  // 64 lanes per 32 rows
+        return dim3((unsigned)(g > 65536 ? 65536 : g));
+    };
     if (kp.splits <= 4)
-        hipLaunchKernelGGL((attn_merge_kernel<D, 4>), dim3((int)g), dim3(256), 0, stream, kp);
+        hipLaunchKernelGGL((attn_merge_kernel<D, 4, 4>), grid(4), dim3(256), 0, stream, kp);
     else if (kp.splits <= 8)
-        hipLaunchKernelGGL((attn_merge_kernel<D, 8>), dim3((int)g), dim3(256), 0, stream, kp);
+        hipLaunchKernelGGL((attn_merge_kernel<D, 8, 4>), grid(4), dim3(256), 0, stream, kp);
     else if (kp.splits <= 16)
-        hipLaunchKernelGGL((attn_merge_kernel<D, 16>), dim3((int)g), dim3(256), 0, stream, kp);
+        hipLaunchKernelGGL((attn_merge_kernel<D, 16, 2>), grid(2), dim3(256), 0, stream, kp);
     else
-        hipLaunchKernelGGL((attn_merge_kernel<D, 64>), dim3((int)g), dim3(256), 0, stream, kp);
+        hipLaunchKernelGGL((attn_merge_kernel<D, 64, 1>), grid(1), dim3(256), 0, stream, kp);
     return hipGetLastError();
 }
 
