@@ -81,13 +81,13 @@ constexpr int ROWS_PER_WAVE = 32;
 constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
 constexpr float RESCALE_TH = 8.0f;  // log2 units
 constexpr float LOG2E = 1.4426950408889634f;
-constexpr int SEG_PAGES = 1024;
+constexpr int SEG_PAGES = 1024;  // block-table entries held in LDS at a time (16384 keys)
 // Block-table entries every wave of the DMA path holds in registers from the start.
 constexpr int WIN_PAGES = 128;
 // LDS fragment reads kept in flight ahead of the MFMA that consumes them: the
 // LDS latency is several MFMA issue slots, and the compiler's own schedule
 // issues each read just one MFMA ahead.
-constexpr int AHEAD = 4;  // block-table entries held in LDS at a time (16384 keys)
+constexpr int AHEAD = 4;
 constexpr uint32_t RSRC_W3 = 0x00020000u;  // buffer resource word 3 (raw, 32-bit elements)
 
 enum { LD_DMA = 0, LD_REG = 1, LD_VALID = 2 };
@@ -519,13 +519,23 @@ __device__ __forceinline__ void load_segment(const int32_t *bt_b, int32_t seg_p0
     for (int k = 0; k < SEG_PAGES / 256; ++k) pt[threadIdx.x + k * 256] = v[k];
 }
 
+// Workgroups a CU holds.  At head_dim 128 the unmasked DMA kernel runs three
+// (a three-stage ring, 52 KB of LDS and at most 168 VGPRs each; the few
+// values that do not fit live outside the key loop): a third wave per SIMD
+// hides more of each tile's latency.  The masked and register-staged
+// variants would spill inside the loop there, so they keep two.
+template <int D, int MASK, int LD>
+constexpr int wg_per_cu() {
+    return D == 128 && LD == LD_DMA && MASK == EMB_MASK_FULL ? 3 : Geo<D>::MIN_WG;
+}
+
 template <int D, int MASK, int LD, bool QF32>
-__global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams p) {
+__global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_kernel(KParams p) {
     using G = Geo<D>;
     constexpr bool VALID = LD == LD_VALID;
     // four stages when the copies bypass registers (a tile's loads get two
-    // iterations to land), three otherwise
-    constexpr int NST = LD == LD_DMA ? 4 : 3;
+    // iterations to land), three otherwise and where three workgroups share a CU
+    constexpr int NST = LD == LD_DMA && wg_per_cu<D, MASK, LD>() < 3 ? 4 : 3;
     __shared__ __attribute__((aligned(16))) uint16_t smem[NST * G::STAGE];
     __shared__ __attribute__((aligned(16))) int32_t pt[VALID ? 4 : SEG_PAGES];
 
@@ -939,11 +949,11 @@ __global__ __launch_bounds__(256, Geo<D>::MIN_WG) void paged_attn_kernel(KParams
             for (int n = 0; n < DmaPlan<D>::PER_TILE; ++n) dma.copy(dsc, st_l, n);
         }
         if constexpr (LD == LD_DMA) {
-            // tile t+2 (needed by the next S) has landed; tile t+3 may still
-            // fly; after the last tile nothing may (the epilogue reuses the
-            // stages)
+            // tile t+2 (needed by the next S) has landed; with four stages
+            // tile t+3, issued this tile, may still fly; after the last tile
+            // nothing may (the epilogue reuses the stages)
             if (t + 1 < t_hi)
-                wait_vmcnt<DmaPlan<D>::PER_TILE>();
+                wait_vmcnt<(NST - 3) * DmaPlan<D>::PER_TILE>();
             else
                 wait_vmcnt<0>();
         } else if (more) {
