@@ -423,6 +423,47 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
                 flops_per_layer=fl_layer, layers=n_layers, splits=best, split_sweep_us_per_layer=sweep)
 
 
+def bench_meta(c: Ctx, steps, n_layers=30):
+    """Runtime-KV slot metadata per layer call at the config-3 shape (14040 slots,
+    1560-token chunks, steady state: every call evicts the oldest chunk).
+    Device: one emb_dev_cache_update (mode 2, slots + valid list in device
+    memory) per layer, 30 layers' caches, graph-timed.  Host: the reference's
+    order per layer -- the host cache's update_meta_only and
+    collect_valid_slots, then synchronous host-to-device copies of the slots
+    and the valid list (models/lingbot_va.cpp:9568-9650, :9697-9767) --
+    wall-clock timed."""
+    torch, emb = c.torch, c.emb
+    cap, C = 14040, 1560
+    dev = [emb.DevSlotCache(cap, c.dev) for _ in range(n_layers)]
+    host = [emb.SlotCache(cap) for _ in range(n_layers)]
+    for _ in range(10):  # past the point where the window is full
+        for d in dev:
+            d.update(C, 2)
+        for h in host:
+            h.update_meta(C, 0)
+    torch.cuda.synchronize()
+
+    def dev_step(st):
+        for d in dev:
+            d.update(C, 2, stream=st)
+    ms, _ = c.time_graph(dev_step, max(2, steps // 4), 2)
+    dev_us = ms * 1e3 / n_layers
+    slots_d = torch.empty(C, dtype=torch.int32, device=c.dev)
+    valid_d = torch.empty(cap, dtype=torch.int32, device=c.dev)
+    reps = max(2, steps // 4)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for h in host:
+            sl, rc = h.update_meta(C, 0)
+            vl = h.collect_valid()
+            slots_d.copy_(torch.from_numpy(sl.astype(np.int32)))
+            valid_d.copy_(torch.from_numpy(vl.astype(np.int32)))
+            torch.cuda.synchronize()
+    host_us = (time.perf_counter() - t0) * 1e6 / (reps * n_layers)
+    return dict(dev_us_per_layer_call=dev_us, host_us_per_layer_call=host_us, capacity=cap, chunk=C,
+                layers=n_layers)
+
+
 def _bf16_bits(f: np.ndarray) -> np.ndarray:
     """float32 -> bf16 bits, round to nearest even (finite inputs)."""
     u = np.ascontiguousarray(f, np.float32).view(np.uint32).astype(np.uint64)
@@ -718,6 +759,7 @@ def main():
     if "cfg3" in cfgs:
         log("cfg3 ...")
         extra["cfg3"] = bench_cfg3(c, args.steps, args.warmup)
+        extra["cfg3"]["slot_metadata"] = bench_meta(c, args.steps)
         log("cfg3", json.dumps(extra["cfg3"]))
     if "cfg5" in cfgs:
         log("cfg5 ...")

@@ -48,6 +48,11 @@ class AttnArgs(C.Structure):
 EMB_GGML_F32, EMB_GGML_F16, EMB_GGML_BF16 = 0, 1, 30
 
 
+class DevCacheDesc(C.Structure):
+    _fields_ = [("id", vp), ("mask", vp), ("is_pred", vp), ("capacity", C.c_int32),
+                ("legacy_clear_pred", C.c_int32)]
+
+
 class GgmlTensor(C.Structure):
     _fields_ = [("type", C.c_int32), ("ne", C.c_int64 * 4), ("nb", C.c_size_t * 4), ("data", vp)]
 
@@ -66,6 +71,10 @@ _SIGS = {
     "emb_slot_cache_prepare_mode0": (C.c_int, [vp, C.c_int64, i64p, i64p, i64p]),
     "emb_slot_cache_restore": (None, [vp, i64p, C.c_int64]),
     "emb_slot_cache_clear_pred": (None, [vp]),
+    "emb_dev_cache_init": (C.c_int, [C.POINTER(DevCacheDesc), vp]),
+    "emb_dev_cache_update": (C.c_int, [C.POINTER(DevCacheDesc), C.c_int32, C.c_int32, vp, vp, vp, vp, vp]),
+    "emb_dev_cache_restore": (C.c_int, [C.POINTER(DevCacheDesc), vp, C.c_int32, vp]),
+    "emb_dev_cache_clear_pred": (C.c_int, [C.POINTER(DevCacheDesc), vp]),
     "emb_slot_cache_collect_valid": (C.c_int64, [vp, i64p]),
     "emb_slot_cache_export": (C.c_int, [vp, i64p, u8p, u8p]),
     "emb_page_pool_create": (vp, [C.c_int32, C.c_uint64]),
@@ -187,6 +196,42 @@ def stream_ptr(stream=None) -> int | None:
 def _np_i64(n):
     a = np.zeros(max(int(n), 1), dtype=np.int64)
     return a, a.ctypes.data_as(i64p)
+
+
+class DevSlotCache:
+    """emb_dev_cache_*: slot metadata in device memory (torch tensors on `device`).
+    update() returns device tensors (slots, valid, n_valid, status); nothing
+    is synchronised."""
+
+    def __init__(self, capacity: int, device, legacy_clear_pred: bool = False, stream=None):
+        import torch
+        self.capacity = capacity
+        self.id = torch.empty(capacity, dtype=torch.int64, device=device)
+        self.mask = torch.empty(capacity, dtype=torch.uint8, device=device)
+        self.is_pred = torch.empty(capacity, dtype=torch.uint8, device=device)
+        self.slots = torch.empty(capacity, dtype=torch.int32, device=device)
+        self.valid = torch.empty(capacity, dtype=torch.int32, device=device)
+        self.n_valid = torch.empty(1, dtype=torch.int32, device=device)
+        self.status = torch.empty(1, dtype=torch.int32, device=device)
+        self.desc = DevCacheDesc(ptr(self.id), ptr(self.mask), ptr(self.is_pred), capacity, int(legacy_clear_pred))
+        check(lib().emb_dev_cache_init(C.byref(self.desc), stream_ptr(stream)), "emb_dev_cache_init")
+
+    def update(self, key_size, mode, stream=None, with_valid=True):
+        check(lib().emb_dev_cache_update(C.byref(self.desc), key_size, mode, ptr(self.slots),
+                                         ptr(self.valid) if with_valid else None,
+                                         ptr(self.n_valid) if with_valid else None, ptr(self.status),
+                                         stream_ptr(stream)), "emb_dev_cache_update")
+        return self.slots[:key_size], self.valid, self.n_valid, self.status
+
+    def restore(self, slots, n, stream=None):
+        check(lib().emb_dev_cache_restore(C.byref(self.desc), ptr(slots), n, stream_ptr(stream)),
+              "emb_dev_cache_restore")
+
+    def clear_pred(self, stream=None):
+        check(lib().emb_dev_cache_clear_pred(C.byref(self.desc), stream_ptr(stream)), "emb_dev_cache_clear_pred")
+
+    def state(self):
+        return self.id.cpu().numpy(), self.mask.cpu().numpy(), self.is_pred.cpu().numpy()
 
 
 class SlotCache:

@@ -146,6 +146,41 @@ int emb_kv_gather(const void *k_pool, const void *v_pool, const int32_t *valid, 
                   int32_t n_kv_heads, int32_t head_dim, hipStream_t stream);
 
 /* ============================================================
+ * Device-resident slot metadata: the same LingBotKVCache semantics as the
+ * host cache above, kept in device memory and updated by kernels, so the
+ * slots and the valid-slot list reach the append and the attention on the
+ * stream with no host scan and no synchronous copy.  Replaces, per layer and
+ * call, the host metadata update under the global runtime-KV mutex plus the
+ * cudaMemcpy of slots and valid_slots in
+ * run_lingbot_runtime_kv_device_attention (models/lingbot_va.cpp:9568-9650,
+ * :9697-9767).  The arrays are caller-owned device memory of `capacity`
+ * entries; emb_dev_cache_init sets every slot empty (id -1, mask 0, is_pred 0).
+ * Eviction ties (equal ids) go in ascending slot order, as in the host cache.
+ * Calls on one cache are stream-ordered; concurrent calls on one cache race.
+ * ============================================================ */
+typedef struct emb_dev_slot_cache {
+    int64_t *id;          /* device [capacity]: insertion id, -1 = empty */
+    uint8_t *mask;        /* device [capacity]: 1 = visible */
+    uint8_t *is_pred;     /* device [capacity]: inserted in mode 1 */
+    int32_t capacity;
+    int32_t legacy_clear_pred; /* VLA_LINGBOT_RUNTIME_KV_LEGACY_CLEAR_PRED semantics */
+} emb_dev_slot_cache;
+
+int emb_dev_cache_init(const emb_dev_slot_cache *c, hipStream_t stream);
+/* One runtime-KV metadata call with key_size new keys.  mode 1 / 2:
+ * update_meta_only (:8887-8902) with pred = (mode == 1), then
+ * collect_valid_slots (:8967-8972); mode 0: prepare_mode0_temp_slots_no_insert
+ * (:8904-8944).  Device outputs: slots[key_size] (ascending), valid[capacity]
+ * (may be NULL) and *n_valid (may be NULL), *status = 0, or EMB_ERR_CAPACITY
+ * when even evicting every visible slot leaves fewer than key_size free (the
+ * evictions stay, as in allocate_slots_into, :8793-8831). */
+int emb_dev_cache_update(const emb_dev_slot_cache *c, int32_t key_size, int32_t mode, int32_t *slots,
+                         int32_t *valid, int32_t *n_valid, int32_t *status, hipStream_t stream);
+int emb_dev_cache_restore(const emb_dev_slot_cache *c, const int32_t *slots, int32_t n,
+                          hipStream_t stream);                                   /* :8946-8952 */
+int emb_dev_cache_clear_pred(const emb_dev_slot_cache *c, hipStream_t stream);   /* :8954-8965 */
+
+/* ============================================================
  * Paged block-masked attention (one launch for a batch of sequences)
  * ============================================================ */
 enum {

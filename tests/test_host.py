@@ -176,6 +176,16 @@ def test_device_entry_points_reject_bad_arguments(emb):
         emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=1, hq=8, hkv=1, d=128,
                             max_q=4, scale=0.1, capacity=64, splits=4, n_keys_uniform=40)
     assert L.lingbot_runtime_kv_attn_f32(None, None, None, None, None, 1, 1, 1, 64, 0.1, None) == -1
+    # device slot metadata: descriptor and call arguments are checked before any launch
+    dc = emb.DevCacheDesc(256, 256, 256, 0, 0)
+    assert L.emb_dev_cache_init(C.byref(dc), None) == -1 and "capacity" in emb.last_error()
+    dc = emb.DevCacheDesc(256, 256, 256, 64, 0)
+    assert L.emb_dev_cache_update(C.byref(dc), 0, 2, buf, None, None, buf, None) == -1
+    assert L.emb_dev_cache_update(C.byref(dc), 4, 3, buf, None, None, buf, None) == -1
+    assert "mode" in emb.last_error()
+    assert L.emb_dev_cache_update(C.byref(dc), 4, 1, None, None, None, buf, None) == -1
+    assert L.emb_dev_cache_restore(C.byref(dc), None, 4, None) == -1
+    assert L.emb_dev_cache_clear_pred(None, None) == -1
     # f16 partial rows (O/l) plus f32 (m, l) per row
     assert emb.attn_workspace_bytes(1, 51, 8, 1, 256, 4) == 4 * 512 * (256 * 2 + 2 * 4)
     # whole-tensor faces: null pointers, head sizes past 256, ggml descriptors
