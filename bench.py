@@ -523,8 +523,31 @@ def bench_cfg5(c: Ctx, steps, warmup):
                             bt_stride=pages, splits=att_splits, workspace=ws, stream=st)
     ms_f, _ = c.time_graph(fused, steps, warmup)
     ms_s, _ = c.time_graph(step, max(2, steps // 4), 2)
+
+    # Cosmos3-style producer: the plain GEMM, then per-head q/k RMSNorm + RoPE
+    # (positions 0..M-1) with the K/V append, one launch (emb_qkv_norm_rope_append)
+    qg = torch.from_numpy(_bf16_bits(g.uniform(0.5, 1.5, d).astype(np.float32)).view(np.int16)).to(c.dev)
+    kg = torch.from_numpy(_bf16_bits(g.uniform(0.5, 1.5, d).astype(np.float32)).view(np.int16)).to(c.dev)
+
+    def norm_rope(st):
+        emb.qkv_norm_rope_append(y, N, M, H, H, d, qo, slots, bt, cap, kp, vp, v16_pool=v16, q_gamma=qg,
+                                 k_gamma=kg, eps=1e-6, rope_kind=1, rope_theta=1e6, first_position=0, stream=st)
+
+    def norm_rope_many(st):
+        for _ in range(k_launch):
+            norm_rope(st)
+    ms_nr, _ = c.time_graph(norm_rope_many, max(2, steps // 4), 2)
+
+    def gemm_norm_rope(st):
+        gemm(st)
+        norm_rope(st)
+    ms_gnr, _ = c.time_graph(gemm_norm_rope, steps, warmup)
+    nr_bytes = M * N * 2 + M * H * d * 2 + 2 * M * H * d * 2 + M * H * d * 2  # read QKV; write Q, K, V, V shadow
     gemm_bytes = M * K * 2 + K * N + N * 2 + M * N * 2
-    return dict(gemm_us=gemm_us, gemm_us_single_launch=ms_g * 1e3, gemm_tflops=flops / (gemm_us * 1e-6) / 1e12,
+    return dict(norm_rope_append_us=ms_nr * 1e3 / k_launch,
+                norm_rope_append_gbs=nr_bytes / (ms_nr * 1e-3 / k_launch) / 1e9,
+                gemm_plus_norm_rope_append_us=ms_gnr * 1e3,
+                gemm_us=gemm_us, gemm_us_single_launch=ms_g * 1e3, gemm_tflops=flops / (gemm_us * 1e-6) / 1e12,
                 gemm_mfma_frac=flops / (gemm_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, gemm_flops=flops,
                 gemm_bytes=gemm_bytes, fused_qkv_append_us=ms_f * 1e3,
                 fused_plus_attention_us_per_layer=ms_s * 1e3)

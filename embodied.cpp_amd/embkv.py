@@ -97,6 +97,9 @@ _SIGS = {
     "emb_self_token_mask": (C.c_int, [vp, u8p]),
     "emb_kv_append": (C.c_int, [vp, vp, C.c_int64, C.c_int32, vp, vp, C.c_int32, vp, vp, vp,
                                 C.c_int32, C.c_int32, vp]),
+    "emb_qkv_norm_rope_append": (C.c_int, [vp, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp,
+                                           C.c_float, C.c_int32, C.c_float, C.c_int32, vp, vp, C.c_int64, vp,
+                                           vp, C.c_int32, vp, vp, vp, vp]),
     "emb_kv_gather": (C.c_int, [vp, vp, vp, C.c_int32, vp, C.c_int32, vp, vp, C.c_int32,
                                 C.c_int32, vp]),
     "emb_attn_workspace_bytes": (C.c_size_t, [C.c_int32] * 6),
@@ -336,6 +339,16 @@ def kv_append(k_new, v_new, src_stride, n, slots, block_table, capacity, k_pool,
     return check(lib().emb_kv_append(ptr(k_new), ptr(v_new), src_stride, n, ptr(slots),
                                      ptr(block_table), capacity, ptr(k_pool), ptr(v_pool),
                                      ptr(v16_pool), hkv, d, stream_ptr(stream)), "emb_kv_append")
+
+
+def qkv_norm_rope_append(qkv, ld, tokens, q_heads, kv_heads, d, q_out, slots, block_table, capacity, k_pool,
+                         v_pool, v16_pool=None, q_gamma=None, k_gamma=None, eps=1e-6, rope_kind=0,
+                         rope_theta=1e6, first_position=0, position_ids=None, ldq=None, stream=None):
+    return check(lib().emb_qkv_norm_rope_append(ptr(qkv), ld, tokens, q_heads, kv_heads, d, ptr(q_gamma),
+                                                 ptr(k_gamma), eps, rope_kind, rope_theta, first_position,
+                                                 ptr(position_ids), ptr(q_out), ldq or q_heads * d, ptr(slots),
+                                                 ptr(block_table), capacity, ptr(k_pool), ptr(v_pool),
+                                                 ptr(v16_pool), stream_ptr(stream)), "emb_qkv_norm_rope_append")
 
 
 def kv_gather(k_pool, v_pool, valid, n, block_table, capacity, k_out, v_out, hkv, d, stream=None):

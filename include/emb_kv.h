@@ -181,6 +181,29 @@ int emb_dev_cache_restore(const emb_dev_slot_cache *c, const int32_t *slots, int
 int emb_dev_cache_clear_pred(const emb_dev_slot_cache *c, hipStream_t stream);   /* :8954-8965 */
 
 /* ============================================================
+ * Per-head q/k RMSNorm + RoPE + paged append, one launch after the QKV
+ * projection: replaces cosmos3_qwen_head_rmsnorm_f32 (Q and K),
+ * cosmos3_qwen_rope_f32 / cosmos3_qwen_mrope_f32 (Q and K) and the cache
+ * update (models/cosmos3.cpp:4967-5012; kernels/cosmos3/
+ * cosmos3_qwen_language_cuda.h:21-52, .cu:52-153).
+ * qkv: bf16 [tokens][ld], per row q_heads Q heads, then kv_heads K heads, then
+ * kv_heads V heads, head_dim each (the layout emb_w8a16_gemm writes for a
+ * concatenated [Wq | Wk | Wv]).  Q and K: RMSNorm over each head with bf16
+ * gamma[head_dim] (NULL gamma: no norm), then RoPE: rope_kind 0 none, 1
+ * position first_position + token, 2 MRoPE with position_ids [3][tokens]
+ * (int32).  Q goes to q_out (bf16 [tokens][ldq]); K and V go into the paged
+ * cache at slots[token] (same rules and layout as emb_kv_append, f16 V shadow
+ * when v16_pool is given).  bf16 rounding points as the reference.
+ * ============================================================ */
+int emb_qkv_norm_rope_append(const void *qkv, int64_t ld, int32_t tokens, int32_t q_heads,
+                             int32_t kv_heads, int32_t head_dim, const uint16_t *q_gamma,
+                             const uint16_t *k_gamma, float eps, int32_t rope_kind, float rope_theta,
+                             int32_t first_position, const int32_t *position_ids, void *q_out,
+                             int64_t ldq, const int32_t *slots, const int32_t *block_table,
+                             int32_t capacity, void *k_pool, void *v_pool, void *v16_pool,
+                             hipStream_t stream);
+
+/* ============================================================
  * Paged block-masked attention (one launch for a batch of sequences)
  * ============================================================ */
 enum {

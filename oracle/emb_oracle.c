@@ -800,3 +800,50 @@ int orc_cpu_attention_f32(const float *q, const float *k, const float *v, int64_
     }
     return used;
 }
+
+/* ---------------- Qwen per-head q/k RMSNorm + RoPE ----------------
+ * kernels/cosmos3/cosmos3_qwen_language_cuda.cu:52-83 (head_rmsnorm_kernel),
+ * :85-116 (rope_kernel), :117-153 (mrope_kernel).  f32 arithmetic with the
+ * reference's bf16 rounding points; sin/cos/pow from libm in f32. */
+static float orc_round_bf16(float f) { return orc_bf16_to_f32(orc_f32_to_bf16(f)); }
+
+void orc_head_norm_rope(const uint16_t *x, int64_t ld, int64_t tokens, int64_t heads, int64_t d,
+                        const uint16_t *gamma, float eps, int rope_kind, float theta, int64_t first_pos,
+                        const int32_t *pos_ids, uint16_t *out, int64_t out_ld) {
+    float *v = (float *)malloc(sizeof(float) * (size_t)d);
+    const int64_t half = d / 2;
+    for (int64_t t = 0; t < tokens; ++t) {
+        for (int64_t h = 0; h < heads; ++h) {
+            const uint16_t *xr = x + t * ld + h * d;
+            if (gamma) {
+                float sum = 0.0f;
+                for (int64_t i = 0; i < d; ++i) {
+                    const float a = orc_bf16_to_f32(xr[i]);
+                    sum += a * a;
+                }
+                const float inv = 1.0f / sqrtf(sum / (float)d + eps);
+                for (int64_t i = 0; i < d; ++i)
+                    v[i] = orc_round_bf16(orc_round_bf16(orc_bf16_to_f32(xr[i]) * inv) * orc_bf16_to_f32(gamma[i]));
+            } else {
+                for (int64_t i = 0; i < d; ++i) v[i] = orc_bf16_to_f32(xr[i]);
+            }
+            uint16_t *o = out + t * out_ld + h * d;
+            for (int64_t i = 0; i < d; ++i) {
+                if (!rope_kind) {
+                    o[i] = orc_f32_to_bf16(v[i]);
+                    continue;
+                }
+                const int64_t p = i < half ? i : i - half;
+                int axis = 0;
+                if (rope_kind == 2 && p < 60) axis = p % 3 == 1 ? 1 : (p % 3 == 2 ? 2 : 0);
+                const float pos = rope_kind == 2 ? (float)pos_ids[axis * tokens + t] : (float)(first_pos + t);
+                const float f = powf(theta, -(float)(2 * p) / (float)d);
+                const float a = pos * f;
+                const float sn = orc_round_bf16(sinf(a)), cs = orc_round_bf16(cosf(a));
+                const float r = i < half ? -v[i + half] : v[i - half];
+                o[i] = orc_f32_to_bf16(v[i] * cs + r * sn);
+            }
+        }
+    }
+    free(v);
+}

@@ -144,6 +144,22 @@ void    orc_w8a16_gemm(const uint16_t *x, const int32_t *qweight, const uint16_t
                        int64_t M, int64_t K, int64_t N, const int64_t *rows, int64_t n_rows,
                        int threads, uint16_t *y_bf16, float *y_f32);
 
+/* ---------------- Qwen per-head q/k RMSNorm + RoPE (Cosmos3 language tower) ----------------
+ * One part (Q or K) of a projection output x, bf16 [tokens][width] with
+ * `heads` heads of head_dim d starting at column 0 of each row.
+ *   norm  (kernels/cosmos3/cosmos3_qwen_language_cuda.cu:52-83), when gamma != NULL:
+ *     inv = 1/sqrt(sum_d x^2 / d + eps); v = bf16(bf16(x * inv) * gamma)
+ *   rope  (:85-116 simple, position first_pos + token; :117-153 MRoPE, position
+ *     pos_ids[axis * tokens + token] with axis 1 / 2 for pair dims p < 60 with
+ *     p % 3 == 1 / 2, else axis 0), when rope_kind != 0:
+ *     p = d' mod (d/2), f = theta^(-2p/d), a = pos * f, s = bf16(sin a),
+ *     c = bf16(cos a), y = bf16(v * c + r * s), r = -v[d' + d/2] below d/2,
+ *     v[d' - d/2] above.
+ * Output bf16 [tokens][heads][d] (row stride out_ld). */
+void orc_head_norm_rope(const uint16_t *x, int64_t ld, int64_t tokens, int64_t heads, int64_t d,
+                        const uint16_t *gamma, float eps, int rope_kind, float theta, int64_t first_pos,
+                        const int32_t *pos_ids, uint16_t *out, int64_t out_ld);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,8 @@ _SIGS = {
                                   C.c_int64, C.c_int64, C.c_int64, C.c_float]),
     "orc_runtime_kv_attn": (None, [f32p, f32p, f32p, i32p, f32p, C.c_int64, C.c_int64, C.c_int64,
                                    C.c_int64, C.c_float, C.c_int]),
+    "orc_head_norm_rope": (None, [u16p, C.c_int64, C.c_int64, C.c_int64, C.c_int64, u16p, C.c_float, C.c_int,
+                                  C.c_float, C.c_int64, i32p, u16p, C.c_int64]),
     "orc_gqa_attention_bf16": (None, [u16p, u16p, u16p, C.c_int64, C.c_int64, C.c_int64,
                                       C.c_int64, C.c_int64, C.c_float, u8p, f32p, C.c_int64,
                                       C.c_int64, C.c_int64, i64p, C.c_int64, C.c_int, f32p]),
@@ -332,3 +334,17 @@ def w8a16_gemm(x, qweight, s_stored, M, K, N, rows=None, threads=0):
     lib().orc_w8a16_gemm(P(x, u16p), P(qweight, i32p), P(s_stored, u16p), M, K, N, P(r, i64p),
                          nr, threads, P(yb, u16p), P(yf, f32p))
     return yb.reshape(nr, N), yf.reshape(nr, N)
+
+
+# ---------------- Qwen per-head q/k RMSNorm + RoPE ----------------
+def head_norm_rope(x, tokens, heads, d, gamma=None, eps=1e-6, rope_kind=0, theta=1e6, first_pos=0,
+                   pos_ids=None, ld=None):
+    """bf16 bits x [tokens][ld] (heads*d columns used) -> bf16 bits [tokens][heads][d]."""
+    x = np.ascontiguousarray(x, np.uint16)
+    ld = ld or heads * d
+    out = np.zeros(tokens * heads * d, np.uint16)
+    g = None if gamma is None else np.ascontiguousarray(gamma, np.uint16)
+    pid = None if pos_ids is None else np.ascontiguousarray(pos_ids, np.int32)
+    lib().orc_head_norm_rope(P(x, u16p), ld, tokens, heads, d, P(g, u16p), C.c_float(eps), rope_kind,
+                             C.c_float(theta), first_pos, P(pid, i32p), P(out, u16p), heads * d)
+    return out.reshape(tokens, heads, d)

@@ -347,3 +347,77 @@ def test_marlin_pack_unpack_and_gemm(orc):
     ref = (orc.bf16_to_f32(x).astype(np.float64) @ w.astype(np.float64)) * orc.bf16_to_f32(s)[None].astype(np.float64)
     assert np.allclose(yf, ref, rtol=1e-6, atol=1e-5)
     assert np.array_equal(yb, orc.f32_to_bf16(yf))
+
+
+# ---------------- Qwen per-head q/k RMSNorm + RoPE ----------------
+def _bf(orc, rng, shape, scale=1.0):
+    return orc.f32_to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def test_head_norm_invariants(orc):
+    rng = np.random.default_rng(31)
+    T, H, D = 5, 3, 128
+    x = _bf(orc, rng, (T, H * D))
+    one = orc.f32_to_bf16(np.ones(D, np.float32))
+    y = orc.bf16_to_f32(orc.head_norm_rope(x, T, H, D, gamma=one, eps=0.0)).astype(np.float64)
+    assert np.allclose(np.sqrt((y ** 2).mean(-1)), 1.0, atol=4e-3)  # unit RMS per head
+    # scaling a head by a power of two leaves the normalised head unchanged (eps 0: exact)
+    x4 = orc.f32_to_bf16(orc.bf16_to_f32(x) * np.float32(4.0))
+    assert np.array_equal(orc.head_norm_rope(x4, T, H, D, gamma=one, eps=0.0),
+                          orc.head_norm_rope(x, T, H, D, gamma=one, eps=0.0))
+    # gamma multiplies after the normalisation: gamma = 2 doubles the unit-gamma result exactly
+    two = orc.f32_to_bf16(np.full(D, 2.0, np.float32))
+    assert np.array_equal(orc.bf16_to_f32(orc.head_norm_rope(x, T, H, D, gamma=two, eps=0.0)),
+                          2 * orc.bf16_to_f32(orc.head_norm_rope(x, T, H, D, gamma=one, eps=0.0)))
+
+
+def test_rope_invariants_and_axis_rule(orc):
+    rng = np.random.default_rng(32)
+    T, H, D = 6, 2, 128
+    x = _bf(orc, rng, (T, H * D))
+    xr = x.reshape(T, H, D)
+    # position 0 is the identity; the rotation keeps each (d, d + D/2) pair's length
+    y = orc.head_norm_rope(x, T, H, D, rope_kind=1, first_pos=0)
+    assert np.array_equal(y[0], xr[0])
+    y = orc.bf16_to_f32(orc.head_norm_rope(x, T, H, D, rope_kind=1, theta=10000.0, first_pos=7)).astype(np.float64)
+    xf = orc.bf16_to_f32(xr).astype(np.float64)
+    n_in = np.hypot(xf[..., :D // 2], xf[..., D // 2:])
+    n_out = np.hypot(y[..., :D // 2], y[..., D // 2:])
+    assert np.allclose(n_out, n_in, rtol=2e-2, atol=2e-2)
+    # pair p rotates by pos * theta^(-2p/D): p = 0 by pos radians (float64 check, bf16 sin/cos)
+    pos = 7 + np.arange(T)
+    c0, s0 = np.cos(pos), np.sin(pos)
+    want = xf[:, :, 0] * c0[:, None] - xf[:, :, D // 2] * s0[:, None]
+    assert np.allclose(y[:, :, 0], want, atol=3e-2)
+    # MRoPE with the same positions on all three axes is the plain RoPE
+    ids = np.tile(7 + np.arange(T, dtype=np.int32), 3)
+    assert np.array_equal(orc.head_norm_rope(x, T, H, D, rope_kind=2, theta=10000.0, pos_ids=ids),
+                          orc.head_norm_rope(x, T, H, D, rope_kind=1, theta=10000.0, first_pos=7))
+    # axis rule (cosmos3_qwen_language_cuda.cu:131-136): only axis 1 nonzero ->
+    # exactly the pairs p < 60 with p % 3 == 1 rotate
+    ids = np.zeros(3 * T, np.int32)
+    ids[T:2 * T] = 5
+    y = orc.head_norm_rope(x, T, H, D, rope_kind=2, theta=10000.0, pos_ids=ids)
+    p = np.arange(D) % (D // 2)
+    moved = (y != xr).any(axis=(0, 1))
+    assert np.array_equal(moved, (p < 60) & (p % 3 == 1))
+
+
+def test_head_norm_rope_matches_numpy(orc):
+    """float64 numpy of the same formula with the reference's bf16 rounding points: within 1 bf16 ulp."""
+    rng = np.random.default_rng(33)
+    T, H, D, eps, theta = 4, 2, 64, 1e-6, 5e5
+    x = _bf(orc, rng, (T, H * D), 3.0)
+    g = _bf(orc, rng, (D,), 0.5)
+    got = orc.bf16_to_f32(orc.head_norm_rope(x, T, H, D, gamma=g, eps=eps, rope_kind=1, theta=theta, first_pos=3))
+    rb = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(np.asarray(a, np.float32)))
+    xf = orc.bf16_to_f32(x).reshape(T, H, D).astype(np.float64)
+    inv = 1.0 / np.sqrt((xf ** 2).mean(-1, keepdims=True) + eps)
+    v = rb(rb(xf * inv) * orc.bf16_to_f32(g)).astype(np.float64)
+    pidx = np.arange(D) % (D // 2)
+    a = (3 + np.arange(T))[:, None] * theta ** (-2.0 * pidx / D)[None, :]
+    c, s = rb(np.cos(a)).astype(np.float64), rb(np.sin(a)).astype(np.float64)
+    r = np.concatenate([-v[..., D // 2:], v[..., :D // 2]], axis=-1)
+    want = rb(v * c[:, None, :] + r * s[:, None, :])
+    ulp = np.abs(want) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(got - want) <= ulp)
