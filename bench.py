@@ -464,6 +464,29 @@ def bench_meta(c: Ctx, steps, n_layers=30):
                 layers=n_layers)
 
 
+def bench_cosmos3_gqa(c: Ctx, steps, warmup):
+    """Cosmos3 language-tower causal GQA attention through the reference-named face
+    (cosmos3_qwen_causal_gqa_attention_f32): 3200 packed text + vision + action tokens,
+    32 query heads over 8 kv heads, head_dim 128, f32 in and out (staging of the f32
+    K/V into the paged pool and the bf16 rounding of the output included)."""
+    torch, emb = c.torch, c.emb
+    T, HQ, HKV, D = 3200, 32, 8, 128
+    q = torch.randn((T, HQ * D), dtype=torch.float32, device=c.dev, generator=torch.Generator(c.dev).manual_seed(5))
+    k = torch.randn((T, HKV * D), dtype=torch.float32, device=c.dev, generator=torch.Generator(c.dev).manual_seed(6))
+    v = torch.randn((T, HKV * D), dtype=torch.float32, device=c.dev, generator=torch.Generator(c.dev).manual_seed(7))
+    y = torch.empty((T, HQ * D), dtype=torch.float32, device=c.dev)
+    L = emb.lib()
+
+    def run(st):
+        emb.check(L.cosmos3_qwen_causal_gqa_attention_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), y.data_ptr(),
+                                                          T, HQ * D, HKV * D, HQ, HKV, D, emb.stream_ptr(st)),
+                  "cosmos3_qwen_causal_gqa_attention_f32")
+    ms, _ = c.time_graph(run, steps, warmup)
+    flops = 4.0 * HQ * D * T * (T + 1) / 2  # causal: key j <= query i
+    return dict(us=ms * 1e3, tflops=flops / (ms * 1e-3) / 1e12, mfma_frac=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                tokens=T, q_heads=HQ, kv_heads=HKV, head_dim=D)
+
+
 def _bf16_bits(f: np.ndarray) -> np.ndarray:
     """float32 -> bf16 bits, round to nearest even (finite inputs)."""
     u = np.ascontiguousarray(f, np.float32).view(np.uint32).astype(np.uint64)
@@ -717,7 +740,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the attention step has no multi-GPU path here; see DESIGN.md for how it would shard)",
+              "(the attention step has no multi-GPU path here; it would shard by session or by kv head)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -788,6 +811,9 @@ def main():
         log("cfg5 ...")
         extra["cfg5"] = bench_cfg5(c, args.steps, args.warmup)
         log("cfg5", json.dumps(extra["cfg5"]))
+        # the Cosmos3 language tower's causal GQA attention face (models/cosmos3.cpp:5032)
+        extra["cosmos3_causal_gqa"] = bench_cosmos3_gqa(c, args.steps, args.warmup)
+        log("cosmos3_causal_gqa", json.dumps(extra["cosmos3_causal_gqa"]))
 
     cpu = None
     if not args.no_cpu:

@@ -349,6 +349,83 @@ int flex_common(const float *q, const float *k, const float *v, const int *row_p
     return EMB_OK;
 }
 
+// Cosmos3 language-tower GQA attention over whole f32 tensors
+// (kernels/cosmos3/cosmos3_qwen_language_cuda.cu:246-298 causal, :371-425 and
+// :938-976 generated tokens over every key, wrappers :1078-1136): q [n_q][hidden],
+// k/v [n_kv][kv], query head h reads kv head h / (q_heads / kv_heads), scale
+// 1/sqrt(head_dim), causal (key j visible to query i iff j <= i) or full, and
+// the output rounded to bf16 values.  K/V are staged into identity-paged pools
+// (with the f16 shadow) and the paged attention runs: the causal mask is the
+// chunk mask with chunk 1.
+__global__ __launch_bounds__(256) void round_bf16_kernel(float *__restrict__ y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = __builtin_bit_cast(float, (uint32_t)to_bf16(y[i]) << 16);
+}
+
+int cosmos3_gqa(const float *q, const float *k, const float *v, float *y, int n_q, int n_kv, int hidden, int kv,
+                int q_heads, int kv_heads, int head_dim, bool causal, hipStream_t stream) {
+    EMB_CHECK_ARG(q && k && v && y, "null pointer");
+    EMB_CHECK_ARG(n_q > 0 && n_kv > 0 && hidden > 0 && kv > 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0,
+                  "non-positive size");
+    EMB_CHECK_ARG(hidden == q_heads * head_dim && kv == kv_heads * head_dim && q_heads % kv_heads == 0,
+                  "hidden / kv do not match the head counts");
+    if (head_dim > 256) return emb::set_error(EMB_ERR_UNSUPPORTED, "head_dim above 256");
+    Plan pl{};
+    pl.batch = 1;
+    pl.n_q = n_q;
+    pl.n_kv = n_kv;
+    pl.hq = q_heads;
+    pl.hkv = kv_heads;
+    pl.d_src = head_dim;
+    pl.dp = padded_dim(head_dim);
+    pl.pps = (n_kv + 15) / 16;
+    pl.kv_batch = 1;
+    const bool padded = pl.dp != head_dim;
+    pl.stage_q = padded || !aligned16(q);
+    pl.stage_out = padded || !aligned16(y);
+    pl.layout();
+    char *ws = nullptr;
+    int rc = face_workspace(pl.total, &ws);
+    if (rc) return rc;
+    const Src4 sk{(const char *)k, 4, (int64_t)kv * 4, (int64_t)head_dim * 4, 0, EMB_GGML_F32};
+    const Src4 sv{(const char *)v, 4, (int64_t)kv * 4, (int64_t)head_dim * 4, 0, EMB_GGML_F32};
+    if ((rc = stage_kv(pl, sk, sv, ws, stream))) return rc;
+    emb_attn_args a;
+    base_args(pl, ws, 1.0f / std::sqrt((float)head_dim), a);
+    if (pl.stage_q) {
+        const Src4 sq{(const char *)q, 4, (int64_t)hidden * 4, (int64_t)head_dim * 4, 0, EMB_GGML_F32};
+        const int64_t total = (int64_t)n_q * q_heads * pl.dp;
+        hipLaunchKernelGGL(stage_q_kernel, dim3(grid_for(total)), dim3(256), 0, stream, sq, n_q, q_heads, head_dim,
+                           pl.dp, 1, (uint16_t *)(ws + pl.off_q));
+        if ((rc = launch_check("stage_q"))) return rc;
+        a.q = ws + pl.off_q;
+        a.q_is_f32 = 0;
+        a.q_stride = (int64_t)q_heads * pl.dp;
+    } else {
+        a.q = q;
+        a.q_is_f32 = 1;
+        a.q_stride = hidden;
+    }
+    a.out = pl.stage_out ? (float *)(ws + pl.off_out) : y;
+    a.out_stride = (int64_t)q_heads * pl.dp;
+    if (causal) {  // query i at key position i (q_pos0 = n_kv - n_q = 0 for self-attention)
+        a.mask_kind = EMB_MASK_CHUNK;
+        a.chunk = 1;
+        a.window = -1;
+    }
+    if ((rc = emb_paged_attention(&a, stream))) return rc;
+    if (pl.stage_out) {
+        const int64_t total = (int64_t)n_q * q_heads * head_dim;
+        hipLaunchKernelGGL(scatter_out_kernel, dim3(grid_for(total)), dim3(256), 0, stream,
+                           (const float *)(ws + pl.off_out), n_q, q_heads, pl.dp, head_dim, 1, (char *)y, (int64_t)4,
+                           (int64_t)head_dim * 4, (int64_t)hidden * 4, (int64_t)0);
+        if ((rc = launch_check("scatter_out"))) return rc;
+    }
+    const int64_t n = (int64_t)n_q * hidden;
+    hipLaunchKernelGGL(round_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, stream, y, n);
+    return launch_check("round_bf16");
+}
+
 int ggml_type_ok(int32_t t) { return t == EMB_GGML_F32 || t == EMB_GGML_F16 || t == EMB_GGML_BF16; }
 size_t ggml_esize(int32_t t) { return t == EMB_GGML_F32 ? 4 : 2; }
 
@@ -572,6 +649,19 @@ int emb_ggml_flash_attn_ext(const emb_ggml_tensor *q, const emb_ggml_tensor *k, 
         if ((rc = launch_check("scatter_out"))) return rc;
     }
     return EMB_OK;
+}
+
+int cosmos3_qwen_causal_gqa_attention_f32(const float *q, const float *k, const float *v, float *y, int tokens,
+                                          int hidden, int kv, int q_heads, int kv_heads, int head_dim,
+                                          hipStream_t stream) {
+    return cosmos3_gqa(q, k, v, y, tokens, tokens, hidden, kv, q_heads, kv_heads, head_dim, true, stream);
+}
+
+int cosmos3_qwen_gen_full_gqa_attention_f32(const float *q_gen, const float *k_all, const float *v_all, float *y_gen,
+                                            int gen_tokens, int all_tokens, int hidden, int kv, int q_heads,
+                                            int kv_heads, int head_dim, hipStream_t stream) {
+    return cosmos3_gqa(q_gen, k_all, v_all, y_gen, gen_tokens, all_tokens, hidden, kv, q_heads, kv_heads, head_dim,
+                       false, stream);
 }
 
 }  // extern "C"

@@ -203,6 +203,22 @@ int emb_qkv_norm_rope_append(const void *qkv, int64_t ld, int32_t tokens, int32_
                              int32_t capacity, void *k_pool, void *v_pool, void *v16_pool,
                              hipStream_t stream);
 
+/* Reference-named Cosmos3 language-tower attention faces
+ * (kernels/cosmos3/cosmos3_qwen_language_cuda.h:77-112, called from
+ * models/cosmos3.cpp:5032,7889,8187): f32 q [tokens][hidden], k/v
+ * [tokens][kv], GQA (query head h reads kv head h / (q_heads / kv_heads)),
+ * scale 1/sqrt(head_dim), output f32 rounded to bf16 values.  causal: key j
+ * visible to query i iff j <= i; gen_full: every generated token sees all
+ * all_tokens keys.  head_dim <= 256.  The first call at a new size allocates
+ * the faces' grow-only workspace (not under stream capture). */
+int cosmos3_qwen_causal_gqa_attention_f32(const float *q, const float *k, const float *v, float *y,
+                                          int tokens, int hidden, int kv, int q_heads, int kv_heads,
+                                          int head_dim, hipStream_t stream);
+int cosmos3_qwen_gen_full_gqa_attention_f32(const float *q_gen, const float *k_all, const float *v_all,
+                                            float *y_gen, int gen_tokens, int all_tokens, int hidden,
+                                            int kv, int q_heads, int kv_heads, int head_dim,
+                                            hipStream_t stream);
+
 /* ============================================================
  * Paged block-masked attention (one launch for a batch of sequences)
  * ============================================================ */

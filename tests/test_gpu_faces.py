@@ -165,3 +165,42 @@ def test_ggml_rejects_unsupported(emb, torch_dev):
                                      emb.ptr(buf), nb, None) == -4  # ALiBi
     kbad = emb.ggml_tensor(buf, emb.EMB_GGML_F16, [64, 8, 3, 1])  # 2 q heads over 3 kv heads
     assert L.emb_ggml_flash_attn_ext_workspace(C.byref(q), C.byref(kbad), C.byref(kbad), None, C.byref(o)) == 0
+
+
+@pytest.mark.parametrize("D,hq,hkv", [(128, 8, 2), (64, 4, 4), (96, 6, 3)])
+def test_cosmos3_gqa_faces(emb, orc, torch_dev, D, hq, hkv):
+    """cosmos3_qwen_causal_gqa_attention_f32 and cosmos3_qwen_gen_full_gqa_attention_f32
+    (kernels/cosmos3/cosmos3_qwen_language_cuda.cu:246-298, :371-425): f32 tensors,
+    GQA, causal or full, output rounded to bf16 values."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(D * 7 + hq)
+    T, G = 300, 51
+    bf = lambda shape: orc.f32_to_bf16(rng.standard_normal(shape).astype(np.float32))
+    q, k, v = bf((T, hq, D)), bf((T, hkv, D)), bf((T, hkv, D))
+    f = lambda a: torch.from_numpy(orc.bf16_to_f32(a).reshape(a.shape[0], -1).copy()).to(dev)
+    L = emb.lib()
+    qd, kd, vd = f(q), f(k), f(v)  # kept alive while the launches run
+    y = torch.full((T, hq * D), float("nan"), dtype=torch.float32, device=dev)
+    rc = L.cosmos3_qwen_causal_gqa_attention_f32(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), y.data_ptr(),
+                                                 T, hq * D, hkv * D, hq, hkv, D, None)
+    assert rc == 0, emb.last_error()
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert np.array_equal(got, orc.bf16_to_f32(orc.f32_to_bf16(got))), "output not rounded to bf16"
+    # the reference rounds its output to bf16 values: so is the oracle's here
+    rb = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(a))
+    ref = rb(orc.gqa_attention(q, k, v, T, T, hq, hkv, D, 1 / math.sqrt(D), chunk=1))
+    assert_close(got.reshape(T, hq, D), ref, "causal")
+    # generated tokens (the last G) over every key
+    yg = torch.full((G, hq * D), float("nan"), dtype=torch.float32, device=dev)
+    qg = q[T - G:]
+    qgd = f(qg)
+    rc = L.cosmos3_qwen_gen_full_gqa_attention_f32(qgd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                                   yg.data_ptr(), G, T, hq * D, hkv * D, hq, hkv, D, None)
+    assert rc == 0, emb.last_error()
+    torch.cuda.synchronize()
+    ref = rb(orc.gqa_attention(qg, k, v, G, T, hq, hkv, D, 1 / math.sqrt(D)))
+    assert_close(yg.cpu().numpy().reshape(G, hq, D), ref, "gen full")
+    assert L.cosmos3_qwen_causal_gqa_attention_f32(None, None, None, None, T, hq * D, hkv * D, hq, hkv, D, None) == -1
+    assert L.cosmos3_qwen_causal_gqa_attention_f32(y.data_ptr(), y.data_ptr(), y.data_ptr(), y.data_ptr(), T,
+                                                   hq * D + 1, hkv * D, hq, hkv, D, None) == -1
