@@ -565,6 +565,27 @@ def bench_cfg5(c: Ctx, steps, warmup):
         gemm(st)
         norm_rope(st)
     ms_gnr, _ = c.time_graph(gemm_norm_rope, steps, warmup)
+    # LingBot post-attention projection with the gated residual in its epilogue
+    # (emb_w8a16_gated_residual): f32 attention output [1560][3072] in, W8 O
+    # weights, gate from a [1560][6*3072] timestep projection, in place on x
+    No = H * d
+    qwo = torch.from_numpy(g.integers(1, 256, (K // 16, 16 * No), dtype=np.uint8).view(np.int32)).to(c.dev)
+    sco = torch.from_numpy(_bf16_bits(g.uniform(0.001, 0.01, No).astype(np.float32)).view(np.int16)).to(c.dev)
+    tproj = torch.randn((M, 6 * No), dtype=torch.float32, device=c.dev)
+    ssh = torch.randn(6 * No, dtype=torch.float32, device=c.dev)
+    ob = torch.randn(No, dtype=torch.float32, device=c.dev)
+    xres = torch.randn((M, No), dtype=torch.float32, device=c.dev)
+    actx = out.view(M, No)
+    xws = torch.empty(M * K, dtype=torch.int16, device=c.dev)
+
+    def oproj_many(st):
+        for _ in range(k_launch):
+            emb.w8a16_gated_residual(actx, qwo, sco, M, K, No, xres, xres, bias=ob, gate=tproj[:, 2 * No:],
+                                     ldg=6 * No, gate_bias=ssh[2 * No:3 * No], x_is_f32=True,
+                                     x_bf16_workspace=xws, stream=st)
+    ms_op, _ = c.time_graph(oproj_many, max(2, steps // 4), 2)
+    op_us = ms_op * 1e3 / k_launch
+    op_flops = 2.0 * M * K * No
     nr_bytes = M * N * 2 + M * H * d * 2 + 2 * M * H * d * 2 + M * H * d * 2  # read QKV; write Q, K, V, V shadow
     gemm_bytes = M * K * 2 + K * N + N * 2 + M * N * 2
     return dict(norm_rope_append_us=ms_nr * 1e3 / k_launch,
@@ -573,7 +594,9 @@ def bench_cfg5(c: Ctx, steps, warmup):
                 gemm_us=gemm_us, gemm_us_single_launch=ms_g * 1e3, gemm_tflops=flops / (gemm_us * 1e-6) / 1e12,
                 gemm_mfma_frac=flops / (gemm_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, gemm_flops=flops,
                 gemm_bytes=gemm_bytes, fused_qkv_append_us=ms_f * 1e3,
-                fused_plus_attention_us_per_layer=ms_s * 1e3)
+                fused_plus_attention_us_per_layer=ms_s * 1e3,
+                oproj_gated_residual_us=op_us, oproj_gated_residual_tflops=op_flops / (op_us * 1e-6) / 1e12,
+                oproj_gated_residual_mfma_frac=op_flops / (op_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS)
 
 
 class MT64:

@@ -37,9 +37,15 @@
 // n_kv to the V pages of a paged KV pool (emb_kv.h layout), at logical slot
 // slots[m] of the token -- the append of runtime_kv_update (kernels/lingbot/
 // lingbot_flex_attn_cuda.cu:626-649) fused into the projection, and the f16 V
-// shadow when one is given.
+// shadow when one is given.  Gated-residual mode is the projection after
+// attention with the block's residual update in the epilogue (the LingBot
+// post graph, models/lingbot_va.cpp:11693-11695, with lin() at :1178-1180):
+//   out[m][n] = x_in[m][n] + ((acc * s[n]) + bias[n]) * (gate[m][n] + gate_bias[n]),
+// each operation rounded to f32 as the graph's separate add/mul nodes do (no
+// fused multiply-add), optionally rounded to bf16 (the graph's bf16 boundary).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <type_traits>
 
@@ -58,7 +64,7 @@ constexpr int AS = BK + 8;  // bf16 elements per staged x row (bank spread)
 constexpr int A_ELEMS = BM * AS;
 constexpr int B_ELEMS = (BK / 16) * BN * 2 * 8;  // [band][n][h][8] bf16
 
-enum { Y_BF16 = 0, Y_F32_ROUNDED = 1, Y_F32_RAW = 2, Y_QKV = 3 };
+enum { Y_BF16 = 0, Y_F32_ROUNDED = 1, Y_F32_RAW = 2, Y_QKV = 3, Y_GATED = 4 };
 
 struct GParams {
     const void *x;
@@ -74,6 +80,13 @@ struct GParams {
     const int32_t *slots;
     const int32_t *bt;
     uint16_t *k_pool, *v_pool, *v16_pool;
+    // gated-residual mode (y is the f32 output)
+    const float *bias, *gate, *gate_bias, *res;
+    int64_t ldg, ldr;
+    int32_t round_out;
+    // f32 x: when set, x is first rounded into this bf16 [M][K] buffer and the
+    // GEMM reads that (the same bf16 values the in-kernel rounding gives)
+    uint16_t *x_ws;
 };
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
@@ -367,6 +380,50 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
         store_cols(std::integral_constant<int, 1>{});
         return;
     }
+    if constexpr (MODE == Y_GATED) {
+        // Per (row block i, column j): all 16 residual and gate loads first
+        // (rows past M clamped to M - 1, so every load is in bounds and none
+        // waits on a branch), then the arithmetic and the stores.
+        auto body = [&](auto gated) __attribute__((always_inline)) {
+#pragma clang fp contract(off)
+            constexpr bool G = decltype(gated)::value;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int32_t n = n0 + wn * 64 + j * 32 + lrow;
+                if (n >= p.N) continue;
+                const float s = __builtin_bit_cast(float, (uint32_t)p.scales[(n >> 5) * 32 + ((n & 31) >> 3) * 2 +
+                                                                            ((n & 7) >> 1) * 8 + (n & 1)]
+                                                                 << 16);
+                const float bn = p.bias ? p.bias[n] : 0.0f;
+                const float gb = G && p.gate_bias ? p.gate_bias[n] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float rv[16], gv[16];
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int32_t m = min(m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3), p.M - 1);
+                        rv[r] = p.res[(int64_t)m * p.ldr + n];
+                        if constexpr (G) gv[r] = p.gate[(int64_t)m * p.ldg + n];
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int32_t m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                        float a = acc[i][j][r] * s;
+                        if (p.bias) a = a + bn;
+                        if constexpr (G) a = a * (gv[r] + gb);
+                        float v = rv[r] + a;
+                        if (p.round_out) v = __builtin_bit_cast(float, f32_to_bf16_bits(v) << 16);
+                        if (m < p.M) reinterpret_cast<float *>(p.y)[(int64_t)m * p.ldy + n] = v;
+                    }
+                }
+            }
+        };
+        if (p.gate)
+            body(std::integral_constant<bool, true>{});
+        else
+            body(std::integral_constant<bool, false>{});
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int32_t n = n0 + wn * 64 + j * 32 + lrow;
@@ -396,6 +453,22 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// f32 [M][ldx] -> bf16 [M][K] (round to nearest even), four elements a thread.
+// Rounding once here instead of while staging keeps the GEMM's prefetch of
+// the next k-tile in flight: the staging path has to wait for its f32 loads
+// before it can convert them, inside the loop.
+__global__ void rows_to_bf16_kernel(const float *x, int64_t ldx, int32_t M, int32_t K, uint16_t *y) {
+    const int32_t q = K / 4;
+    const int64_t total = (int64_t)M * q;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t m = i / q, c = (i % q) * 4;
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(x + m * ldx + c);
+        *reinterpret_cast<u32x2 *>(y + m * K + c) =
+            u32x2{f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16),
+                  f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16)};
+    }
+}
+
 template <bool XF32, int MODE>
 hipError_t launch(const GParams &p, hipStream_t stream) {
     const int total = p.m_tiles * p.n_tiles;
@@ -416,11 +489,24 @@ int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
     p.m_tiles = (p.M + BM - 1) / BM;
     p.n_tiles = (p.N + BN - 1) / BN;
     hipError_t e;
+    if (xf32 && p.x_ws) {
+        EMB_CHECK_ARG(aligned16(p.x_ws), "x_bf16_workspace must be 16-byte aligned");
+        const int64_t units = (int64_t)p.M * (p.K / 4);
+        const int64_t g = std::min<int64_t>((units + 255) / 256, 8192);
+        hipLaunchKernelGGL(rows_to_bf16_kernel, dim3((unsigned)g), dim3(256), 0, stream, (const float *)p.x, p.ldx,
+                           p.M, p.K, p.x_ws);
+        e = hipGetLastError();
+        if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "x rounding launch: %s", hipGetErrorString(e));
+        p.x = p.x_ws;
+        p.ldx = p.K;
+        xf32 = false;
+    }
     if (xf32) {
         switch (mode) {
             case Y_BF16: e = launch<true, Y_BF16>(p, stream); break;
             case Y_F32_ROUNDED: e = launch<true, Y_F32_ROUNDED>(p, stream); break;
             case Y_F32_RAW: e = launch<true, Y_F32_RAW>(p, stream); break;
+            case Y_GATED: e = launch<true, Y_GATED>(p, stream); break;
             default: e = launch<true, Y_QKV>(p, stream); break;
         }
     } else {
@@ -428,6 +514,7 @@ int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
             case Y_BF16: e = launch<false, Y_BF16>(p, stream); break;
             case Y_F32_ROUNDED: e = launch<false, Y_F32_ROUNDED>(p, stream); break;
             case Y_F32_RAW: e = launch<false, Y_F32_RAW>(p, stream); break;
+            case Y_GATED: e = launch<false, Y_GATED>(p, stream); break;
             default: e = launch<false, Y_QKV>(p, stream); break;
         }
     }
@@ -505,11 +592,57 @@ int emb_w8a16_qkv_append(const void *x, int32_t x_is_f32, int64_t ldx, const int
     return run_gemm(p, x_is_f32 != 0, Y_QKV, stream);
 }
 
+int emb_w8a16_gated_residual(const void *x, int32_t x_is_f32, int64_t ldx, const int32_t *qweight,
+                             const uint16_t *scales, int32_t M, int32_t K, int32_t N, const float *bias,
+                             const float *gate, int64_t ldg, const float *gate_bias, const float *residual,
+                             int64_t ldr, float *out, int64_t ldo, int32_t round_bf16, void *x_bf16_workspace,
+                             hipStream_t stream) {
+    EMB_CHECK_ARG(residual && out, "null residual/out");
+    EMB_CHECK_ARG(M > 0 && K > 0 && N > 0, "non-positive size");
+    EMB_CHECK_ARG(ldr >= N && ldo >= N, "ldr and ldo must cover N");
+    EMB_CHECK_ARG(!gate || ldg >= N, "ldg must cover N");
+    EMB_CHECK_ARG(gate || !gate_bias, "gate_bias needs a gate");
+    // out may be the residual itself (each element is read, then written, by
+    // one thread); any other overlap of out with an input is rejected
+    const float *olo = out, *ohi = out + (int64_t)(M - 1) * ldo + N;
+    auto overlaps = [&](const void *q, int64_t bytes) {
+        const char *a = (const char *)q, *b = a + bytes;
+        return q && a < (const char *)ohi && (const char *)olo < b;
+    };
+    EMB_CHECK_ARG(residual == out || !overlaps(residual, ((int64_t)(M - 1) * ldr + N) * 4),
+                  "out overlaps residual without being it");
+    EMB_CHECK_ARG(!overlaps(gate, gate ? ((int64_t)(M - 1) * ldg + N) * 4 : 0) && !overlaps(bias, (int64_t)N * 4) &&
+                      !overlaps(gate_bias, (int64_t)N * 4),
+                  "out overlaps gate or bias");
+    EMB_CHECK_ARG(residual != out || ldr == ldo, "in-place update needs ldr == ldo");
+    GParams p{};
+    p.x = x;
+    p.ldx = ldx;
+    p.qw = reinterpret_cast<const uint32_t *>(qweight);
+    p.scales = scales;
+    p.M = M;
+    p.K = K;
+    p.N = N;
+    p.y = out;
+    p.ldy = ldo;
+    p.bias = bias;
+    p.gate = gate;
+    p.gate_bias = gate_bias;
+    p.res = residual;
+    p.ldg = ldg;
+    p.ldr = ldr;
+    p.round_out = round_bf16 != 0;
+    p.x_ws = (uint16_t *)x_bf16_workspace;
+    return run_gemm(p, x_is_f32 != 0, Y_GATED, stream);
+}
+
 // ---- reference-named face (kernels/cosmos3/cosmos3_w8_marlin_cuda.h:24-84) ----
 // y is f32 holding the bf16-rounded result, as the reference's bf16 -> f32
-// widening (cosmos3_w8_marlin_cuda.cu:407) leaves it.  The workspaces of the
-// _ws variants are accepted and unused: f32 inputs are rounded to bf16 while
-// they are staged, and no split-K reduction buffer is needed.
+// widening (cosmos3_w8_marlin_cuda.cu:407) leaves it.  linear_f32_ws rounds x
+// into x_bf16_workspace first (as the reference does, :446-455) and runs the
+// bf16 GEMM; linear_f32 has no workspace and rounds x while staging it.  The
+// other workspaces are accepted and unused: no split-K reduction buffer is
+// needed.
 
 int cosmos3_w8a16_linear_f32(const float *x, const int *qweight, const unsigned short *scales_bf16, float *y,
                              int batch, int in_features, int out_features, int qweight_rows, int qweight_cols,
@@ -526,12 +659,25 @@ int cosmos3_w8a16_linear_f32_ws(const float *x, const int *qweight, const unsign
                                 float *c_tmp_workspace, int *int_workspace, int batch, int in_features,
                                 int out_features, int qweight_rows, int qweight_cols, int scale_rows, int scale_cols,
                                 hipStream_t stream) {
-    (void)x_bf16_workspace;
     (void)y_bf16_workspace;
     (void)c_tmp_workspace;
     (void)int_workspace;
-    return cosmos3_w8a16_linear_f32(x, qweight, scales_bf16, y, batch, in_features, out_features, qweight_rows,
-                                    qweight_cols, scale_rows, scale_cols, stream);
+    const int rc = check_ref_shapes(batch, in_features, out_features, qweight_rows, qweight_cols, scale_rows,
+                                    scale_cols);
+    if (rc) return rc;
+    EMB_CHECK_ARG(y, "null y");
+    GParams p{};
+    p.x = x;
+    p.ldx = in_features;
+    p.qw = reinterpret_cast<const uint32_t *>(qweight);
+    p.scales = scales_bf16;
+    p.M = batch;
+    p.K = in_features;
+    p.N = out_features;
+    p.y = y;
+    p.ldy = out_features;
+    p.x_ws = x_bf16_workspace;  // rounded once into it, then the bf16 GEMM
+    return run_gemm(p, true, Y_F32_ROUNDED, stream);
 }
 
 int cosmos3_w8a16_linear_bf16_ws(const unsigned short *x_bf16, const int *qweight, const unsigned short *scales_bf16,

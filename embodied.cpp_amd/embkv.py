@@ -130,6 +130,9 @@ _SIGS = {
     "emb_w8a16_qkv_append": (C.c_int, [vp, C.c_int32, C.c_int64, vp, vp, C.c_int32, C.c_int32,
                                        C.c_int32, vp, C.c_int64, vp, vp, C.c_int32, vp, vp, vp,
                                        C.c_int32, C.c_int32, vp]),
+    "emb_w8a16_gated_residual": (C.c_int, [vp, C.c_int32, C.c_int64, vp, vp, C.c_int32, C.c_int32,
+                                           C.c_int32, vp, vp, C.c_int64, vp, vp, C.c_int64, vp,
+                                           C.c_int64, C.c_int32, vp, vp]),
     "cosmos3_w8a16_linear_f32": (C.c_int, [vp, vp, vp, vp] + [C.c_int] * 7 + [vp]),
     "cosmos3_w8a16_linear_f32_ws": (C.c_int, [vp] * 8 + [C.c_int] * 7 + [vp]),
     "cosmos3_w8a16_linear_bf16_ws": (C.c_int, [vp] * 7 + [C.c_int] * 7 + [vp]),
@@ -373,6 +376,44 @@ def w8a16_qkv_append(x, qweight, scales, M, K, n_q, q_out, slots, block_table, c
                                             ptr(slots), ptr(block_table), capacity, ptr(k_pool),
                                             ptr(v_pool), ptr(v16_pool), hkv, d, stream_ptr(stream)),
                  "emb_w8a16_qkv_append")
+
+
+def _need_bytes(t, nbytes, what):
+    """Refuse a torch tensor smaller than the extent a kernel will read or write
+    (a C-ABI call cannot see buffer sizes)."""
+    if t is None or not hasattr(t, "untyped_storage"):
+        return
+    have = t.untyped_storage().nbytes() - t.storage_offset() * t.element_size()  # from data_ptr to the end
+    if have < nbytes:
+        raise ValueError(f"{what}: {have} bytes from its start, {nbytes} needed")
+
+
+def _need_rows(t, rows, ld, cols, esize, what):
+    """Same for a [rows][ld] view: the last row ends at (rows - 1) * ld + cols."""
+    _need_bytes(t, ((rows - 1) * ld + cols) * esize, what)
+
+
+def w8a16_gated_residual(x, qweight, scales, M, K, N, residual, out, bias=None, gate=None,
+                         gate_bias=None, ldg=None, ldr=None, ldo=None, round_bf16=False,
+                         x_is_f32=False, ldx=None, x_bf16_workspace=None, stream=None):
+    """out = residual + ((W8 projection of x) + bias) * (gate + gate_bias), f32
+    (emb_w8a16_gated_residual); out may be the residual tensor itself."""
+    _need_rows(x, M, ldx or K, K, 4 if x_is_f32 else 2, "x")
+    _need_bytes(qweight, (K // 16) * 4 * N * 4, "qweight ([K/16][4N] int32)")
+    _need_bytes(scales, N * 2, "scales")
+    _need_rows(residual, M, ldr or N, N, 4, "residual")
+    _need_rows(out, M, ldo or N, N, 4, "out")
+    _need_rows(gate, M, ldg or N, N, 4, "gate")
+    _need_bytes(bias, N * 4, "bias")
+    _need_bytes(gate_bias, N * 4, "gate_bias")
+    if x_is_f32:
+        _need_bytes(x_bf16_workspace, M * K * 2, "x_bf16_workspace")
+    return check(lib().emb_w8a16_gated_residual(ptr(x), int(x_is_f32), ldx or K, ptr(qweight),
+                                                ptr(scales), M, K, N, ptr(bias), ptr(gate),
+                                                ldg or N, ptr(gate_bias), ptr(residual), ldr or N,
+                                                ptr(out), ldo or N, int(round_bf16),
+                                                ptr(x_bf16_workspace), stream_ptr(stream)),
+                 "emb_w8a16_gated_residual")
 
 
 def attn_workspace_bytes(batch, max_q, hq, hkv, d, splits):

@@ -417,9 +417,36 @@ int emb_w8a16_qkv_append(const void *x, int32_t x_is_f32, int64_t ldx, const int
                          int32_t capacity, void *k_pool, void *v_pool, void *v16_pool,
                          int32_t n_kv_heads, int32_t head_dim, hipStream_t stream);
 
+/* The projection after attention with the block's gated residual update in
+ * its epilogue: replaces lin(o, self_ctx) and x = x_in + a1 * gate_msa of the
+ * LingBot post graph (models/lingbot_va.cpp:11693-11695; lin() :1178-1180;
+ * gate_msa = timestep_proj chunk 2 + scale_shift chunk 2, :11679-11681), with
+ * the O weights in the W8 layout above.
+ *   out[m][n] = residual[m][n] + ((acc[m][n] * s[n]) + bias[n])
+ *                                * (gate[m][n] + gate_bias[n])
+ * acc as in emb_w8a16_gemm (fp32, not rounded to bf16).  Each operation is
+ * rounded to f32 separately (no fused multiply-add), as the graph's add and
+ * mul nodes are.  bias, gate_bias: f32 [N] or NULL (0); gate: f32 [M][ldg]
+ * or NULL (no gate: a plain residual add, gate_bias must then be NULL);
+ * residual f32 [M][ldr]; out f32 [M][ldo], which may be the residual itself
+ * (in place, ldo == ldr) but must not otherwise overlap an input.
+ * round_bf16 != 0 rounds out to bf16 precision (the graph's bf16 boundary,
+ * :11676-11678).  x_bf16_workspace (bf16 [M][K], 16-byte aligned, or NULL):
+ * with f32 x, x is rounded into it first and the GEMM reads it -- the same
+ * values as without it, and faster (the in-kernel rounding stalls the k-tile
+ * prefetch); ignored for bf16 x. */
+int emb_w8a16_gated_residual(const void *x, int32_t x_is_f32, int64_t ldx, const int32_t *qweight,
+                             const uint16_t *scales, int32_t M, int32_t K, int32_t N,
+                             const float *bias, const float *gate, int64_t ldg,
+                             const float *gate_bias, const float *residual, int64_t ldr, float *out,
+                             int64_t ldo, int32_t round_bf16, void *x_bf16_workspace,
+                             hipStream_t stream);
+
 /* Reference-named W8 face (kernels/cosmos3/cosmos3_w8_marlin_cuda.h:24-84 with
- * hipStream_t).  y is f32 holding the bf16-rounded result.  The workspaces of
- * the _ws variants are accepted and not used. */
+ * hipStream_t).  y is f32 holding the bf16-rounded result.  linear_f32_ws
+ * rounds x into x_bf16_workspace (batch * in_features bf16, or NULL: rounded
+ * while staged) before the GEMM, as the reference does; the other workspaces
+ * are accepted and not used. */
 int cosmos3_w8a16_linear_f32(const float *x, const int *qweight, const unsigned short *scales_bf16,
                              float *y, int batch, int in_features, int out_features,
                              int qweight_rows, int qweight_cols, int scale_rows, int scale_cols,

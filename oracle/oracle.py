@@ -336,6 +336,27 @@ def w8a16_gemm(x, qweight, s_stored, M, K, N, rows=None, threads=0):
     return yb.reshape(nr, N), yf.reshape(nr, N)
 
 
+def gated_residual(y, residual, bias=None, gate=None, gate_bias=None, round_bf16=False):
+    """Epilogue of the projection after attention in the LingBot post graph
+    (models/lingbot_va.cpp:11693-11695, lin() :1178-1180, bf16 boundary
+    :11676-11678): a1 = y + bias; x = residual + a1 * (gate + gate_bias), every
+    node an f32 operation of its own.  y is the projection's f32 value ([M][N],
+    e.g. the second result of w8a16_gemm); gate [M][N] or None."""
+    f = np.float32
+    a = np.asarray(y, f)
+    if bias is not None:
+        a = (a + np.asarray(bias, f)[None, :]).astype(f)
+    if gate is not None:
+        g = np.asarray(gate, f)
+        if gate_bias is not None:
+            g = (g + np.asarray(gate_bias, f)[None, :]).astype(f)
+        a = (a * g).astype(f)
+    out = (np.asarray(residual, f) + a).astype(f)
+    if round_bf16:
+        out = bf16_to_f32(f32_to_bf16(out))
+    return out
+
+
 # ---------------- Qwen per-head q/k RMSNorm + RoPE ----------------
 def head_norm_rope(x, tokens, heads, d, gamma=None, eps=1e-6, rope_kind=0, theta=1e6, first_pos=0,
                    pos_ids=None, ld=None):

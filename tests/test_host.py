@@ -157,6 +157,24 @@ def test_device_entry_points_reject_bad_arguments(emb):
     assert "out_features" in emb.last_error()
     assert L.cosmos3_w8a16_linear_f32(buf, buf, buf, buf, 4, 128, 128, 9, 512, 1, 128, None) == -1
     assert L.emb_w8a16_gemm(buf, 0, 128, buf, buf, 4, 128, 128, buf, 128, 7, None) == -1
+    # gated residual: overlaps, strides and gate_bias without a gate are refused
+    G = lambda *a: L.emb_w8a16_gated_residual(*a[:-1], None, a[-1])  # no x workspace
+    o, r = C.c_void_p(1 << 20), C.c_void_p(1 << 24)
+    assert G(buf, 0, 128, buf, buf, 4, 128, 128, None, None, 128, None, None, 128, o, 128, 0, None) == -1
+    assert "null" in emb.last_error()
+    assert G(buf, 0, 128, buf, buf, 4, 128, 128, None, None, 128, buf, r, 128, o, 128, 0, None) == -1
+    assert "gate_bias needs a gate" in emb.last_error()
+    assert G(buf, 0, 128, buf, buf, 4, 128, 128, None, None, 128, None, C.c_void_p((1 << 20) + 512), 128, o, 128,
+             0, None) == -1
+    assert "overlaps residual" in emb.last_error()
+    assert G(buf, 0, 128, buf, buf, 4, 128, 128, None, C.c_void_p((1 << 20) + 64), 768, None, r, 128, o, 128,
+             0, None) == -1
+    assert "overlaps gate" in emb.last_error()
+    assert G(buf, 0, 128, buf, buf, 4, 128, 128, None, None, 128, None, o, 256, o, 128, 0, None) == -1
+    assert "ldr == ldo" in emb.last_error()
+    assert G(buf, 0, 128, buf, buf, 4, 128, 128, None, r, 64, None, r, 128, o, 128, 0, None) == -1
+    assert "ldg" in emb.last_error()
+    assert G(buf, 0, 96, buf, buf, 4, 96, 96, None, None, 96, None, r, 96, o, 96, 0, None) == -4
     assert L.emb_kv_gather(buf, buf, buf, 0, None, 16, buf, buf, 1, 128, None) == -1
     assert L.lingbot_runtime_kv_update_f32(buf, buf, buf, buf, buf, 4, 1, 64, 4, None) == -1
     assert "capacity" in emb.last_error()
@@ -206,3 +224,19 @@ def test_device_entry_points_reject_bad_arguments(emb):
     assert L.emb_ggml_flash_attn_ext(C.byref(q), C.byref(k), C.byref(k), None, 0.1, 0.0, 0.0, C.byref(o),
                                      None, ws, None) == -1  # no workspace
     assert "workspace" in emb.last_error()
+
+
+def test_gated_residual_wrapper_refuses_short_buffers(emb):
+    """The Python face checks tensor extents the C-ABI cannot see: a Marlin
+    weight of [K/16][N] words instead of [K/16][4N] is refused before launch."""
+    import torch
+    M, K, N = 8, 64, 64
+    x = torch.zeros((M, K), dtype=torch.int16)
+    s = torch.zeros(N, dtype=torch.int16)
+    r = torch.zeros((M, N))
+    with pytest.raises(ValueError, match="qweight"):
+        emb.w8a16_gated_residual(x, torch.zeros((K // 16, N), dtype=torch.int32), s, M, K, N, r, r)
+    tp = torch.zeros((M, 6 * N))
+    with pytest.raises(ValueError, match="gate"):  # a gate view at column 5N has too few columns left
+        emb.w8a16_gated_residual(x, torch.zeros((K // 16, 4 * N), dtype=torch.int32), s, M, K, N, r, r,
+                                 gate=tp[:, 5 * N + 1:], ldg=6 * N)

@@ -421,3 +421,50 @@ def test_head_norm_rope_matches_numpy(orc):
     want = rb(v * c[:, None, :] + r * s[:, None, :])
     ulp = np.abs(want) * 2.0 ** -7 + 1e-30
     assert np.all(np.abs(got - want) <= ulp)
+
+
+# ---------------- gated residual (post-attention projection epilogue) ----------------
+def test_gated_residual_special_cases(orc):
+    """No gate and no bias: a plain f32 residual add; gate 1: the same; gate 0
+    with gate_bias 0: the residual unchanged; gate 0 with gate_bias g: the
+    same as gate g; bias shifts y before the gate (not after)."""
+    rng = np.random.default_rng(11)
+    M, N = 7, 64
+    y = rng.standard_normal((M, N)).astype(np.float32)
+    r = rng.standard_normal((M, N)).astype(np.float32) * 3
+    g = rng.standard_normal((M, N)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    assert np.array_equal(orc.gated_residual(y, r), r + y)
+    assert np.array_equal(orc.gated_residual(y, r, gate=np.ones((M, N), np.float32)), r + y)
+    assert np.array_equal(orc.gated_residual(y, r, gate=np.zeros((M, N), np.float32),
+                                             gate_bias=np.zeros(N, np.float32)), r)
+    gb = rng.standard_normal(N).astype(np.float32)
+    assert np.array_equal(orc.gated_residual(y, r, gate=np.zeros((M, N), np.float32), gate_bias=gb),
+                          orc.gated_residual(y, r, gate=np.broadcast_to(gb, (M, N)).copy()))
+    # exact small integers: (y + b) * (g + gb) + r by hand
+    yi = np.array([[3.0, -2.0]], np.float32)
+    out = orc.gated_residual(yi, np.array([[10.0, 1.0]], np.float32), bias=np.array([1.0, 4.0], np.float32),
+                             gate=np.array([[2.0, 0.5]], np.float32), gate_bias=np.array([1.0, 0.5], np.float32))
+    assert np.array_equal(out, np.array([[10.0 + 4.0 * 3.0, 1.0 + 2.0 * 1.0]], np.float32))
+
+
+def test_gated_residual_separate_roundings_and_bf16(orc):
+    """Each node rounds to f32: the result equals the float64 value of the
+    same expression rounded after every step, and differs from a single
+    final rounding somewhere on random data (so a fused form would fail);
+    round_bf16 rounds the f32 result to nearest-even bf16."""
+    rng = np.random.default_rng(12)
+    M, N = 64, 128
+    y, r, g = (rng.standard_normal((M, N)).astype(np.float32) for _ in range(3))
+    b, gb = (rng.standard_normal(N).astype(np.float32) for _ in range(2))
+    out = orc.gated_residual(y, r, bias=b, gate=g, gate_bias=gb)
+    f32 = lambda v: np.float32(v)
+    a1 = f32(y.astype(np.float64) + b)
+    gg = f32(g.astype(np.float64) + gb)
+    want = f32(r.astype(np.float64) + f32(a1.astype(np.float64) * gg))
+    assert np.array_equal(out, want)
+    once = f32(r.astype(np.float64) + (y.astype(np.float64) + b) * (g.astype(np.float64) + gb))
+    assert not np.array_equal(out, once)
+    ob = orc.gated_residual(y, r, bias=b, gate=g, gate_bias=gb, round_bf16=True)
+    import torch
+    assert np.array_equal(ob, torch.from_numpy(out).to(torch.bfloat16).float().numpy())
