@@ -565,6 +565,24 @@ def bench_cfg5(c: Ctx, steps, warmup):
         gemm(st)
         norm_rope(st)
     ms_gnr, _ = c.time_graph(gemm_norm_rope, steps, warmup)
+    # LingBot producer: full-row q/k RMSNorm + Wan RoPE (per-token tables) +
+    # append on the f32 QKV projection row (emb_qkv_rownorm_rope_append)
+    qkv32 = torch.randn((M, N), dtype=torch.float32, device=c.dev)
+    qkb = torch.randn(N, dtype=torch.float32, device=c.dev)
+    qnw = torch.rand(H * d, dtype=torch.float32, device=c.dev) + 0.5
+    knw = torch.rand(H * d, dtype=torch.float32, device=c.dev) + 0.5
+    ang = torch.rand((M, d // 2), dtype=torch.float32, device=c.dev) * 100
+    rc, rs = torch.cos(ang), torch.sin(ang)
+
+    def rownorm_many(st):
+        for _ in range(k_launch):
+            emb.qkv_rownorm_rope_append(qkv32, N, M, H, d, qo, slots, bt, cap, kp, vp, v16_pool=v16, qkv_bias=qkb,
+                                        q_weight=qnw, k_weight=knw, eps=1e-6, rope_cos=rc, rope_sin=rs, stream=st)
+    ms_rn, _ = c.time_graph(rownorm_many, max(2, steps // 4), 2)
+    rn_us = ms_rn * 1e3 / k_launch
+    # read QKV f32, bias, weights, tables; write Q, K, V, V shadow (bf16)
+    rn_bytes = M * N * 4 + N * 4 + 2 * H * d * 4 + 2 * M * (d // 2) * 4 + 4 * M * H * d * 2
+
     # LingBot post-attention projection with the gated residual in its epilogue
     # (emb_w8a16_gated_residual): f32 attention output [1560][3072] in, W8 O
     # weights, gate from a [1560][6*3072] timestep projection, in place on x
@@ -595,6 +613,8 @@ def bench_cfg5(c: Ctx, steps, warmup):
                 gemm_mfma_frac=flops / (gemm_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, gemm_flops=flops,
                 gemm_bytes=gemm_bytes, fused_qkv_append_us=ms_f * 1e3,
                 fused_plus_attention_us_per_layer=ms_s * 1e3,
+                lingbot_rownorm_rope_append_us=rn_us,
+                lingbot_rownorm_rope_append_gbs=rn_bytes / (rn_us * 1e-6) / 1e9,
                 oproj_gated_residual_us=op_us, oproj_gated_residual_tflops=op_flops / (op_us * 1e-6) / 1e12,
                 oproj_gated_residual_mfma_frac=op_flops / (op_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS)
 

@@ -173,6 +173,161 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(NRParams p) {
     }
 }
 
+// ---- LingBot: full-row q/k RMSNorm + Wan RoPE + append (f32 QKV) ----
+//
+// Reference: build_attention_shape (models/lingbot_va.cpp:1219-1250): q =
+// rms_norm(lin(q)) * q_norm_weight over the whole hidden row (all heads at
+// once), k the same, v = lin(v); then apply_wan_rope_shape (:1190-1206) on q
+// and k: per head, pairs (2i, 2i+1) rotated by the per-token tables
+// rope_cos / rope_sin [seq][head_dim/2] (y0 = x0 c - x1 s, y1 = x1 c + x0 s).
+// Everything is f32 (ggml's rms_norm: scale = 1 / sqrt(sum(x^2) / n + eps)),
+// each node rounded on its own (no fused multiply-add); the outputs are
+// rounded to bf16 once, for the bf16 Q buffer and cache.
+constexpr int RN_MAXC = 8;  // float4 chunks a thread holds: hidden <= 8192
+
+struct RNParams {
+    const float *qkv;
+    int64_t ld;
+    int32_t tokens, heads, hd, hidden;
+    const float *bias, *q_w, *k_w;
+    float eps;
+    const float *cs, *sn;  // [tokens][hd/2]
+    uint16_t *q_out;
+    int64_t ldq;
+    const int32_t *slots, *bt;
+    int32_t capacity;
+    uint16_t *k_pool, *v_pool, *v16_pool;
+};
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u32x2 pack_bf16x4(const f32x4_t &v) {
+    return u32x2{bf16_rne(v[0]) | (bf16_rne(v[1]) << 16), bf16_rne(v[2]) | (bf16_rne(v[3]) << 16)};
+}
+
+// Workgroup sum of two values (four waves).
+__device__ __forceinline__ void wg_sum2(float &a, float &b, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        a += __shfl_xor(a, off, 64);
+        b += __shfl_xor(b, off, 64);
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        red[wave * 2] = a;
+        red[wave * 2 + 1] = b;
+    }
+    __syncthreads();
+    a = (red[0] + red[2]) + (red[4] + red[6]);
+    b = (red[1] + red[3]) + (red[5] + red[7]);
+}
+
+__global__ __launch_bounds__(256) void row_norm_rope_append_kernel(RNParams p) {
+#pragma clang fp contract(off)
+    __shared__ float red[8];
+    if ((int32_t)blockIdx.x >= p.tokens) {
+        // V heads: a thread per (token, head, 8-dim chunk), tokens fastest
+        const int64_t idx = (int64_t)(blockIdx.x - p.tokens) * 256 + threadIdx.x;
+        const int CH = p.hd / 8;
+        const int32_t s = (int32_t)(idx % p.tokens);
+        const int64_t hc = idx / p.tokens;
+        const int c = (int)(hc % CH), h = (int)(hc / CH);
+        if (h >= p.heads) return;
+        const int32_t slot = p.slots[s];
+        if (slot < 0 || slot >= p.capacity) return;
+        const int32_t page = p.bt ? p.bt[slot >> 4] : (slot >> 4);
+        if (page < 0) return;
+        const int col = h * p.hd + c * 8;
+        const float *src = p.qkv + (int64_t)s * p.ld + 2 * p.hidden + col;
+        f32x4_t v0 = *reinterpret_cast<const f32x4_t *>(src), v1 = *reinterpret_cast<const f32x4_t *>(src + 4);
+        if (p.bias) {
+            v0 = v0 + *reinterpret_cast<const f32x4_t *>(p.bias + 2 * p.hidden + col);
+            v1 = v1 + *reinterpret_cast<const f32x4_t *>(p.bias + 2 * p.hidden + col + 4);
+        }
+        const int32_t t = slot & 15;
+        const int64_t pbase = ((int64_t)page * p.heads + h) * 16 * p.hd;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t b = bf16_rne(e < 4 ? v0[e] : v1[e - 4]);
+            const int d = c * 8 + e;
+            p.v_pool[pbase + d * 16 + t] = (uint16_t)b;
+            if (p.v16_pool) p.v16_pool[pbase + emb::v16_index(d, t)] = __builtin_bit_cast(uint16_t, (_Float16)bf16f(b));
+        }
+        return;
+    }
+    const int32_t tok = blockIdx.x;
+    const int nch = p.hidden / 4;
+    const float *row = p.qkv + (int64_t)tok * p.ld;
+    f32x4_t q[RN_MAXC], k[RN_MAXC];
+    float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+    for (int j = 0; j < RN_MAXC; ++j) {
+        const int c = threadIdx.x + 256 * j;
+        q[j] = k[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        if (c < nch) {
+            q[j] = *reinterpret_cast<const f32x4_t *>(row + 4 * c);
+            k[j] = *reinterpret_cast<const f32x4_t *>(row + p.hidden + 4 * c);
+            if (p.bias) {
+                q[j] = q[j] + *reinterpret_cast<const f32x4_t *>(p.bias + 4 * c);
+                k[j] = k[j] + *reinterpret_cast<const f32x4_t *>(p.bias + p.hidden + 4 * c);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sq += q[j][e] * q[j][e];
+                sk += k[j][e] * k[j][e];
+            }
+        }
+    }
+    float inv_q = 1.0f, inv_k = 1.0f;
+    if (p.q_w || p.k_w) {
+        wg_sum2(sq, sk, red);
+        inv_q = 1.0f / sqrtf(sq / (float)p.hidden + p.eps);
+        inv_k = 1.0f / sqrtf(sk / (float)p.hidden + p.eps);
+    }
+    int64_t page_base = -1;
+    int32_t trow = 0;
+    {
+        const int32_t slot = p.slots[tok];
+        if (slot >= 0 && slot < p.capacity) {
+            const int32_t page = p.bt ? p.bt[slot >> 4] : (slot >> 4);
+            if (page >= 0) {
+                page_base = (int64_t)page * p.heads * 16 * p.hd;
+                trow = slot & 15;
+            }
+        }
+    }
+    const int half = p.hd / 2;
+#pragma unroll
+    for (int j = 0; j < RN_MAXC; ++j) {
+        const int c = threadIdx.x + 256 * j;
+        if (c >= nch) continue;
+        const int e0 = 4 * c;
+        if (p.q_w) q[j] = (q[j] * inv_q) * *reinterpret_cast<const f32x4_t *>(p.q_w + e0);
+        if (p.k_w) k[j] = (k[j] * inv_k) * *reinterpret_cast<const f32x4_t *>(p.k_w + e0);
+        const int h = e0 / p.hd, d = e0 % p.hd;
+        if (p.cs) {
+            const int pi = d / 2;  // pairs pi, pi + 1 of this chunk
+            const float *cr = p.cs + (int64_t)tok * half + pi, *sr = p.sn + (int64_t)tok * half + pi;
+            const float c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
+            auto rot = [&](f32x4_t &x) {
+#pragma clang fp contract(off)
+                const f32x4_t o = x;
+                x[0] = o[0] * c0 - o[1] * s0;
+                x[1] = o[1] * c0 + o[0] * s0;
+                x[2] = o[2] * c1 - o[3] * s1;
+                x[3] = o[3] * c1 + o[2] * s1;
+            };
+            rot(q[j]);
+            rot(k[j]);
+        }
+        *reinterpret_cast<u32x2 *>(p.q_out + (int64_t)tok * p.ldq + e0) = pack_bf16x4(q[j]);
+        if (page_base >= 0)
+            *reinterpret_cast<u32x2 *>(p.k_pool + page_base + (int64_t)h * 16 * p.hd + trow * p.hd + d) =
+                pack_bf16x4(k[j]);
+    }
+}
+
 inline bool aligned16(const void *q) { return ((uintptr_t)q & 15u) == 0; }
 
 }  // namespace
@@ -207,5 +362,36 @@ extern "C" int emb_qkv_norm_rope_append(const void *qkv, int64_t ld, int32_t tok
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "emb_qkv_norm_rope_append: %s", hipGetErrorString(e));
+    return EMB_OK;
+}
+
+extern "C" int emb_qkv_rownorm_rope_append(const float *qkv, int64_t ld, int32_t tokens, int32_t heads,
+                                           int32_t head_dim, const float *qkv_bias, const float *q_weight,
+                                           const float *k_weight, float eps, const float *rope_cos,
+                                           const float *rope_sin, void *q_out, int64_t ldq, const int32_t *slots,
+                                           const int32_t *block_table, int32_t capacity, void *k_pool,
+                                           void *v_pool, void *v16_pool, hipStream_t stream) {
+    EMB_CHECK_ARG(qkv && q_out && slots && k_pool && v_pool, "null pointer");
+    EMB_CHECK_ARG(tokens > 0 && heads > 0 && capacity > 0, "non-positive size");
+    EMB_CHECK_ARG(head_dim > 0 && head_dim % 8 == 0, "head_dim must be a positive multiple of 8");
+    const int64_t hidden = (int64_t)heads * head_dim;
+    EMB_CHECK_ARG(hidden <= 4 * 256 * RN_MAXC, "heads * head_dim must be at most 8192");
+    EMB_CHECK_ARG(ld >= 3 * hidden && ld % 4 == 0, "ld must cover a QKV row and be a multiple of 4");
+    EMB_CHECK_ARG(ldq >= hidden && ldq % 4 == 0, "ldq must cover a Q row and be a multiple of 4");
+    EMB_CHECK_ARG((rope_cos == nullptr) == (rope_sin == nullptr), "rope_cos and rope_sin go together");
+    EMB_CHECK_ARG(eps >= 0.0f && std::isfinite(eps), "eps must be finite and non-negative");
+    EMB_CHECK_ARG(aligned16(qkv) && aligned16(qkv_bias) && aligned16(q_weight) && aligned16(k_weight),
+                  "qkv, bias and norm weights must be 16-byte aligned");
+    EMB_CHECK_ARG(((uintptr_t)q_out & 7u) == 0 && ((uintptr_t)k_pool & 7u) == 0, "q_out and k_pool must be 8-byte aligned");
+    RNParams p{qkv, ld, tokens, heads, head_dim, (int32_t)hidden, qkv_bias, q_weight, k_weight, eps, rope_cos,
+               rope_sin, (uint16_t *)q_out, ldq, slots, block_table, capacity, (uint16_t *)k_pool,
+               (uint16_t *)v_pool, (uint16_t *)v16_pool};
+    const int64_t v_threads = (int64_t)tokens * heads * (head_dim / 8);
+    EMB_CHECK_ARG(tokens + (v_threads + 255) / 256 < INT32_MAX, "grid too large");
+    hipLaunchKernelGGL(row_norm_rope_append_kernel, dim3((unsigned)(tokens + (v_threads + 255) / 256)), dim3(256), 0,
+                       stream, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return emb::set_error(EMB_ERR_LAUNCH, "emb_qkv_rownorm_rope_append: %s", hipGetErrorString(e));
     return EMB_OK;
 }

@@ -97,6 +97,9 @@ _SIGS = {
     "emb_self_token_mask": (C.c_int, [vp, u8p]),
     "emb_kv_append": (C.c_int, [vp, vp, C.c_int64, C.c_int32, vp, vp, C.c_int32, vp, vp, vp,
                                 C.c_int32, C.c_int32, vp]),
+    "emb_qkv_rownorm_rope_append": (C.c_int, [vp, C.c_int64, C.c_int32, C.c_int32, C.c_int32, vp, vp, vp,
+                                              C.c_float, vp, vp, vp, C.c_int64, vp, vp, C.c_int32, vp, vp,
+                                              vp, vp]),
     "emb_qkv_norm_rope_append": (C.c_int, [vp, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp,
                                            C.c_float, C.c_int32, C.c_float, C.c_int32, vp, vp, C.c_int64, vp,
                                            vp, C.c_int32, vp, vp, vp, vp]),
@@ -354,6 +357,28 @@ def qkv_norm_rope_append(qkv, ld, tokens, q_heads, kv_heads, d, q_out, slots, bl
                                                  ptr(position_ids), ptr(q_out), ldq or q_heads * d, ptr(slots),
                                                  ptr(block_table), capacity, ptr(k_pool), ptr(v_pool),
                                                  ptr(v16_pool), stream_ptr(stream)), "emb_qkv_norm_rope_append")
+
+
+def qkv_rownorm_rope_append(qkv, ld, tokens, heads, d, q_out, slots, block_table, capacity, k_pool, v_pool,
+                            v16_pool=None, qkv_bias=None, q_weight=None, k_weight=None, eps=1e-6,
+                            rope_cos=None, rope_sin=None, ldq=None, stream=None):
+    """LingBot full-row q/k RMSNorm + Wan RoPE (per-token cos/sin tables) + paged
+    K/V append on an f32 QKV row (emb_qkv_rownorm_rope_append)."""
+    hid = heads * d
+    _need_rows(qkv, tokens, ld, 3 * hid, 4, "qkv")
+    _need_rows(q_out, tokens, ldq or hid, hid, 2, "q_out")
+    _need_bytes(qkv_bias, 3 * hid * 4, "qkv_bias")
+    _need_bytes(q_weight, hid * 4, "q_weight")
+    _need_bytes(k_weight, hid * 4, "k_weight")
+    _need_bytes(rope_cos, tokens * (d // 2) * 4, "rope_cos")
+    _need_bytes(rope_sin, tokens * (d // 2) * 4, "rope_sin")
+    _need_bytes(slots, tokens * 4, "slots")
+    return check(lib().emb_qkv_rownorm_rope_append(ptr(qkv), ld, tokens, heads, d, ptr(qkv_bias),
+                                                    ptr(q_weight), ptr(k_weight), eps, ptr(rope_cos),
+                                                    ptr(rope_sin), ptr(q_out), ldq or hid, ptr(slots),
+                                                    ptr(block_table), capacity, ptr(k_pool), ptr(v_pool),
+                                                    ptr(v16_pool), stream_ptr(stream)),
+                 "emb_qkv_rownorm_rope_append")
 
 
 def kv_gather(k_pool, v_pool, valid, n, block_table, capacity, k_out, v_out, hkv, d, stream=None):

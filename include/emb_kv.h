@@ -203,6 +203,30 @@ int emb_qkv_norm_rope_append(const void *qkv, int64_t ld, int32_t tokens, int32_
                              int32_t capacity, void *k_pool, void *v_pool, void *v16_pool,
                              hipStream_t stream);
 
+/* LingBot form of the same step: full-row q/k RMSNorm (over all heads of the
+ * row at once) and Wan RoPE from per-token tables, with the K/V append --
+ * build_attention_shape's q/k/v path (models/lingbot_va.cpp:1219-1250;
+ * apply_wan_rope_shape :1190-1206; lin() :1178-1180) on the f32 projection
+ * output of the QKV graph (:11795-11875), ahead of
+ * lingbot_runtime_kv_update_f32's append (lingbot_flex_attn_cuda.cu:626-649).
+ * qkv: f32 [tokens][ld], columns [0, H*D) q, [H*D, 2H*D) k, [2H*D, 3H*D) v
+ * (H = heads for q and k/v alike); qkv_bias f32 [3*H*D] or NULL, added first
+ * (lin's bias).  q = rms_norm(q) * q_weight, k likewise (f32 [H*D] weights;
+ * NULL skips that norm), scale = 1 / sqrt(sum(x^2) / (H*D) + eps).  RoPE:
+ * rope_cos / rope_sin f32 [tokens][D/2] (both or neither); in each head pair
+ * (2i, 2i+1) becomes (x0 c - x1 s, x1 c + x0 s) with c, s at [token][i].
+ * Every step is an f32 operation of its own; Q goes to q_out bf16
+ * [tokens][ldq], K and V bf16 into the cache at slots[token] (skip rules of
+ * emb_kv_append), f16 V shadow if v16_pool.  Needs D % 8 == 0 and
+ * H*D <= 8192; qkv, bias and weights 16-byte aligned, ld and ldq multiples
+ * of 4. */
+int emb_qkv_rownorm_rope_append(const float *qkv, int64_t ld, int32_t tokens, int32_t heads,
+                                int32_t head_dim, const float *qkv_bias, const float *q_weight,
+                                const float *k_weight, float eps, const float *rope_cos,
+                                const float *rope_sin, void *q_out, int64_t ldq,
+                                const int32_t *slots, const int32_t *block_table, int32_t capacity,
+                                void *k_pool, void *v_pool, void *v16_pool, hipStream_t stream);
+
 /* Reference-named Cosmos3 language-tower attention faces
  * (kernels/cosmos3/cosmos3_qwen_language_cuda.h:77-112, called from
  * models/cosmos3.cpp:5032,7889,8187): f32 q [tokens][hidden], k/v

@@ -357,6 +357,51 @@ def gated_residual(y, residual, bias=None, gate=None, gate_bias=None, round_bf16
     return out
 
 
+# ---------------- LingBot full-row q/k RMSNorm + Wan RoPE ----------------
+def lingbot_row_norm(x, weight, eps=1e-6):
+    """ggml_rms_norm over the whole row then * weight (models/lingbot_va.cpp:
+    1233-1234): scale = 1 / sqrt(sum(x^2) / n + eps) in f32 (the sum taken in
+    float64), y = (x * scale) * weight, f32 [tokens][n]."""
+    f = np.float32
+    x = np.asarray(x, f)
+    ss = (x.astype(np.float64) ** 2).sum(axis=1)
+    scale = (f(1.0) / np.sqrt((ss.astype(f) / f(x.shape[1]) + f(eps)).astype(f))).astype(f)
+    return ((x * scale[:, None]).astype(f) * np.asarray(weight, f)[None, :]).astype(f)
+
+
+def wan_rope(x, heads, d, cos, sin):
+    """apply_wan_rope_shape (models/lingbot_va.cpp:1190-1206): x f32
+    [tokens][heads*d]; in each head pair (2i, 2i+1) -> (x0 c - x1 s, x1 c + x0 s),
+    c = cos[token][i], s = sin[token][i], every product and sum an f32 op."""
+    f = np.float32
+    t = x.shape[0]
+    xp = np.asarray(x, f).reshape(t, heads, d // 2, 2)
+    c = np.asarray(cos, f).reshape(t, 1, d // 2)
+    s = np.asarray(sin, f).reshape(t, 1, d // 2)
+    x0, x1 = xp[..., 0], xp[..., 1]
+    y0 = ((x0 * c).astype(f) - (x1 * s).astype(f)).astype(f)
+    y1 = ((x1 * c).astype(f) + (x0 * s).astype(f)).astype(f)
+    return np.stack([y0, y1], axis=-1).reshape(t, heads * d)
+
+
+def lingbot_qkv(qkv, heads, d, bias=None, q_w=None, k_w=None, eps=1e-6, cos=None, sin=None):
+    """build_attention_shape's q/k/v (models/lingbot_va.cpp:1219-1250) from an
+    f32 projection row [tokens][>= 3*heads*d]: (q, k, v) f32 [tokens][heads*d]."""
+    f = np.float32
+    hid = heads * d
+    x = np.asarray(qkv, f)[:, :3 * hid]
+    if bias is not None:
+        x = (x + np.asarray(bias, f)[None, :]).astype(f)
+    q, k, v = x[:, :hid], x[:, hid:2 * hid], x[:, 2 * hid:]
+    if q_w is not None:
+        q = lingbot_row_norm(q, q_w, eps)
+    if k_w is not None:
+        k = lingbot_row_norm(k, k_w, eps)
+    if cos is not None:
+        q, k = wan_rope(q, heads, d, cos, sin), wan_rope(k, heads, d, cos, sin)
+    return q, k, v
+
+
 # ---------------- Qwen per-head q/k RMSNorm + RoPE ----------------
 def head_norm_rope(x, tokens, heads, d, gamma=None, eps=1e-6, rope_kind=0, theta=1e6, first_pos=0,
                    pos_ids=None, ld=None):

@@ -157,6 +157,16 @@ def test_device_entry_points_reject_bad_arguments(emb):
     assert "out_features" in emb.last_error()
     assert L.cosmos3_w8a16_linear_f32(buf, buf, buf, buf, 4, 128, 128, 9, 512, 1, 128, None) == -1
     assert L.emb_w8a16_gemm(buf, 0, 128, buf, buf, 4, 128, 128, buf, 128, 7, None) == -1
+    # LingBot row norm + RoPE: head_dim, row size and table pairing are checked first
+    R = L.emb_qkv_rownorm_rope_append
+    assert R(buf, 384, 4, 1, 124, None, None, None, 1e-6, None, None, buf, 128, buf, None, 16, buf, buf, None,
+             None) == -1 and "multiple of 8" in emb.last_error()
+    assert R(buf, 3 * 8448, 4, 66, 128, None, None, None, 1e-6, None, None, buf, 8448, buf, None, 16, buf, buf,
+             None, None) == -1 and "8192" in emb.last_error()
+    assert R(buf, 384, 4, 1, 128, None, None, None, 1e-6, buf, None, buf, 128, buf, None, 16, buf, buf, None,
+             None) == -1 and "go together" in emb.last_error()
+    assert R(buf, 380, 4, 1, 128, None, None, None, 1e-6, None, None, buf, 128, buf, None, 16, buf, buf, None,
+             None) == -1 and "ld" in emb.last_error()
     # gated residual: overlaps, strides and gate_bias without a gate are refused
     G = lambda *a: L.emb_w8a16_gated_residual(*a[:-1], None, a[-1])  # no x workspace
     o, r = C.c_void_p(1 << 20), C.c_void_p(1 << 24)

@@ -468,3 +468,60 @@ def test_gated_residual_separate_roundings_and_bf16(orc):
     ob = orc.gated_residual(y, r, bias=b, gate=g, gate_bias=gb, round_bf16=True)
     import torch
     assert np.array_equal(ob, torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+
+
+# ---------------- LingBot full-row RMSNorm + Wan RoPE ----------------
+def test_lingbot_row_norm_invariants(orc):
+    """Unit weight: every row comes out with mean square 1 / (1 + eps / ms)
+    (ms = the input row's mean square), the row's direction unchanged; a
+    per-column weight multiplies column-wise; scaling a row (eps = 0) leaves
+    the result unchanged up to f32 rounding."""
+    rng = np.random.default_rng(41)
+    x = (rng.standard_normal((9, 3072)) * rng.uniform(0.1, 30, (9, 1))).astype(np.float32)
+    y = orc.lingbot_row_norm(x, np.ones(3072, np.float32), eps=1e-6).astype(np.float64)
+    ms = (x.astype(np.float64) ** 2).mean(axis=1)
+    np.testing.assert_allclose((y ** 2).mean(axis=1), ms / (ms + 1e-6), rtol=1e-5)
+    cosang = (y * x).sum(1) / np.linalg.norm(y, axis=1) / np.linalg.norm(x.astype(np.float64), axis=1)
+    np.testing.assert_allclose(cosang, 1.0, rtol=1e-6)
+    w = rng.uniform(0.5, 2, 3072).astype(np.float32)
+    np.testing.assert_allclose(orc.lingbot_row_norm(x, w), y * w, rtol=3e-7, atol=1e-7)
+    np.testing.assert_allclose(orc.lingbot_row_norm(x * np.float32(8), w, eps=0.0),
+                               orc.lingbot_row_norm(x, w, eps=0.0), rtol=1e-6)
+
+
+def test_wan_rope_is_a_complex_rotation(orc):
+    """Each (x0, x1) pair times (c + i s) as a complex product, to f32
+    rounding; c = 1, s = 0 is the identity and c = 0, s = 1 maps a pair to
+    (-x1, x0) exactly; the tables are indexed by token and pair, shared by
+    every head."""
+    rng = np.random.default_rng(42)
+    T, H, D = 5, 3, 16
+    x = rng.standard_normal((T, H * D)).astype(np.float32)
+    ang = rng.uniform(-np.pi, np.pi, (T, D // 2))
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    y = orc.wan_rope(x, H, D, c, s)
+    z = x.astype(np.float64).reshape(T, H, D // 2, 2)
+    zc = (z[..., 0] + 1j * z[..., 1]) * (c.astype(np.float64) + 1j * s.astype(np.float64))[:, None, :]
+    want = np.stack([zc.real, zc.imag], -1).reshape(T, H * D)
+    np.testing.assert_allclose(y, want, rtol=0, atol=4e-7 * np.abs(x).max())
+    one, zero = np.ones((T, D // 2), np.float32), np.zeros((T, D // 2), np.float32)
+    assert np.array_equal(orc.wan_rope(x, H, D, one, zero), x)
+    r = orc.wan_rope(x, H, D, zero, one).reshape(T, H, D // 2, 2)
+    xp = x.reshape(T, H, D // 2, 2)
+    assert np.array_equal(r[..., 0], -xp[..., 1]) and np.array_equal(r[..., 1], xp[..., 0])
+
+
+def test_lingbot_qkv_bias_then_norm(orc):
+    """The bias is added before the norm (lin() then rms_norm); v only gets its
+    bias; with no weights and no tables q and k are the biased projections."""
+    rng = np.random.default_rng(43)
+    T, H, D = 4, 2, 8
+    x = rng.standard_normal((T, 3 * H * D + 5)).astype(np.float32)
+    b = rng.standard_normal(3 * H * D).astype(np.float32)
+    q, k, v = orc.lingbot_qkv(x, H, D, bias=b)
+    xb = x[:, :3 * H * D] + b
+    assert np.array_equal(q, xb[:, :H * D]) and np.array_equal(k, xb[:, H * D:2 * H * D])
+    assert np.array_equal(v, xb[:, 2 * H * D:])
+    w = np.ones(H * D, np.float32)
+    q2, _, _ = orc.lingbot_qkv(x, H, D, bias=b, q_w=w)
+    assert np.array_equal(q2, orc.lingbot_row_norm(xb[:, :H * D], w))
