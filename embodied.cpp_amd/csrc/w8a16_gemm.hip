@@ -26,7 +26,10 @@
 // two operands agree and no byte of W is moved twice.
 //
 // Tiling.  A workgroup of 4 waves (2 x 2) computes a 256 x 128 tile of y; a
-// wave owns 128 x 64 (4 x 2 MFMA blocks, 128 accumulator registers).  K moves
+// wave owns 128 x 64 (4 x 2 MFMA blocks, 128 accumulator registers).  When
+// 256-row tiles would leave CUs idle (fewer tiles than CUs) the tiles are
+// 128 x 128 instead (2 x 2 blocks a wave); each output element sums the same
+// k-steps in the same order either way.  K moves
 // in tiles of 64.  The next k-tile's x and W words are loaded into registers
 // while the current one is multiplied; they are then converted (x: permuted;
 // W: u8 -> bf16(u8 - 128), once per workgroup) and written to the single LDS
@@ -59,9 +62,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 256, BN = 128, BK = 64;
+constexpr int BN = 128, BK = 64;  // tile rows BM (256 or 128) is a template argument
 constexpr int AS = BK + 8;  // bf16 elements per staged x row (bank spread)
-constexpr int A_ELEMS = BM * AS;
+// A stage: BM x AS bf16; B stage:
 constexpr int B_ELEMS = (BK / 16) * BN * 2 * 8;  // [band][n][h][8] bf16
 
 enum { Y_BF16 = 0, Y_F32_ROUNDED = 1, Y_F32_RAW = 2, Y_QKV = 3, Y_GATED = 4 };
@@ -133,16 +136,16 @@ __device__ __forceinline__ void interleave16(const u32x4 &a, const u32x4 &b, u32
     }
 }
 
-template <bool XF32>
+template <bool XF32, int BM>
 struct Stage {
     // x: 4 units of (row, 16-k group); W: two 16-byte runs of one band.
-    u32x4 xa[4], xb[4];
+    u32x4 xa[BM / 64], xb[BM / 64];
     u32x4 w0, w1;
 
     __device__ __forceinline__ void load(const GParams &p, int32_t m0, int32_t n0, int32_t k0) {
         const int tid = threadIdx.x;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < BM / 64; ++i) {
             const int u = tid + i * 256;
             const int row = u >> 2, g = u & 3;
             const int32_t m = m0 + row, k = k0 + g * 16;
@@ -189,7 +192,7 @@ struct Stage {
     __device__ __forceinline__ void store(uint16_t *as, uint16_t *bs) const {
         const int tid = threadIdx.x;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < BM / 64; ++i) {
             const int u = tid + i * 256;
             const int row = u >> 2, g = u & 3;
             u32x4 o0, o1;
@@ -214,9 +217,9 @@ struct Stage {
     }
 };
 
-template <bool XF32, int MODE>
+template <bool XF32, int MODE, int BM>
 __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
-    __shared__ __attribute__((aligned(16))) uint16_t as[A_ELEMS];
+    __shared__ __attribute__((aligned(16))) uint16_t as[BM * AS];
     __shared__ __attribute__((aligned(16))) uint16_t bs[B_ELEMS];
 
     // XCD-aware order: consecutive logical tiles share an n-tile (the same
@@ -231,13 +234,14 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
     const int wm = wave >> 1, wn = wave & 1;
     const int lrow = lane & 31, lhi = lane >> 5;
 
-    f32x16 acc[4][2];
+    constexpr int MI = BM / 64;  // 32-row MFMA blocks a wave holds
+    f32x16 acc[MI][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-    Stage<XF32> st;
+    Stage<XF32, BM> st;
     const int32_t n_kt = (p.K + BK - 1) / BK;
     st.load(p, m0, n0, 0);
     st.store(as, bs);
@@ -250,8 +254,8 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
         for (int ks = 0; ks < BK / 16; ++ks) {
             bf16x8 a[4], bfr[2];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = wm * 128 + i * 32 + lrow;
+            for (int i = 0; i < MI; ++i) {
+                const int row = wm * (BM / 2) + i * 32 + lrow;
                 a[i] = __builtin_bit_cast(
                     bf16x8, *reinterpret_cast<const u32x4 *>(as + row * AS + ks * 16 + lhi * 8));
             }
@@ -263,7 +267,7 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
                                             *reinterpret_cast<const u32x4 *>(bs + ((ks * BN + n) * 2 + slot) * 8));
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bfr[j], acc[i][j], 0, 0, 0);
@@ -311,10 +315,10 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
                                                              << 16);
             if (n < p.n_q) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < MI; ++i)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int32_t m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                        const int32_t m = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
                         if (m < p.M)
                             reinterpret_cast<uint16_t *>(p.y)[(int64_t)m * p.ldy + n] =
                                 (uint16_t)f32_to_bf16_bits(acc[i][j][r] * s);
@@ -327,10 +331,10 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
             const int32_t d = cc % p.head_dim;
             const int64_t hoff = (cc / p.head_dim) * hstride;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int rl = wm * 128 + i * 32 + g * 8 + lhi * 4;  // four consecutive rows
+                    const int rl = wm * (BM / 2) + i * 32 + g * 8 + lhi * 4;  // four consecutive rows
                     int64_t e[4];
                     uint32_t b[4];
 #pragma unroll
@@ -397,17 +401,17 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
                 const float bn = p.bias ? p.bias[n] : 0.0f;
                 const float gb = G && p.gate_bias ? p.gate_bias[n] : 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < MI; ++i) {
                     float rv[16], gv[16];
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int32_t m = min(m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3), p.M - 1);
+                        const int32_t m = min(m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3), p.M - 1);
                         rv[r] = p.res[(int64_t)m * p.ldr + n];
                         if constexpr (G) gv[r] = p.gate[(int64_t)m * p.ldg + n];
                     }
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int32_t m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                        const int32_t m = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
                         float a = acc[i][j][r] * s;
                         if (p.bias) a = a + bn;
                         if constexpr (G) a = a * (gv[r] + gb);
@@ -432,10 +436,10 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
                                                                     ((n & 7) >> 1) * 8 + (n & 1)]
                                                          << 16);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int32_t m = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
+                const int32_t m = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
                 if (m >= p.M) continue;
                 const float v = acc[i][j][r] * s;
                 if (MODE == Y_F32_RAW) {
@@ -469,12 +473,32 @@ __global__ void rows_to_bf16_kernel(const float *x, int64_t ldx, int32_t M, int3
     }
 }
 
-template <bool XF32, int MODE>
+template <bool XF32, int MODE, int BM>
 hipError_t launch(const GParams &p, hipStream_t stream) {
     const int total = p.m_tiles * p.n_tiles;
     const int grid = (total + 7) / 8 * 8;
-    hipLaunchKernelGGL((w8a16_gemm_kernel<XF32, MODE>), dim3(grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((w8a16_gemm_kernel<XF32, MODE, BM>), dim3(grid), dim3(256), 0, stream, p);
     return hipGetLastError();
+}
+
+template <int BM>
+hipError_t dispatch(const GParams &p, bool xf32, int mode, hipStream_t stream) {
+    if (xf32) {
+        switch (mode) {
+            case Y_BF16: return launch<true, Y_BF16, BM>(p, stream);
+            case Y_F32_ROUNDED: return launch<true, Y_F32_ROUNDED, BM>(p, stream);
+            case Y_F32_RAW: return launch<true, Y_F32_RAW, BM>(p, stream);
+            case Y_GATED: return launch<true, Y_GATED, BM>(p, stream);
+            default: return launch<true, Y_QKV, BM>(p, stream);
+        }
+    }
+    switch (mode) {
+        case Y_BF16: return launch<false, Y_BF16, BM>(p, stream);
+        case Y_F32_ROUNDED: return launch<false, Y_F32_ROUNDED, BM>(p, stream);
+        case Y_F32_RAW: return launch<false, Y_F32_RAW, BM>(p, stream);
+        case Y_GATED: return launch<false, Y_GATED, BM>(p, stream);
+        default: return launch<false, Y_QKV, BM>(p, stream);
+    }
 }
 
 int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
@@ -486,8 +510,12 @@ int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
     EMB_CHECK_ARG(p.ldx >= p.K && (p.ldx * (xf32 ? 4 : 2)) % 16 == 0, "x row stride must cover K, 16-byte aligned");
     EMB_CHECK_ARG(aligned16(p.x) && aligned16(p.qw), "x and qweight must be 16-byte aligned");
     EMB_CHECK_ARG((int64_t)p.M * (p.N / 64) < INT_MAX, "problem too large");
-    p.m_tiles = (p.M + BM - 1) / BM;
+    // 256-row tiles, unless they leave CUs idle (fewer tiles than the 256 CUs,
+    // e.g. the 3072-wide O-projection over 1560 rows: 168 tiles); then
+    // 128-row tiles, twice as many, each half the work
     p.n_tiles = (p.N + BN - 1) / BN;
+    const bool narrow = (int64_t)((p.M + 255) / 256) * p.n_tiles < 256;
+    p.m_tiles = narrow ? (p.M + 127) / 128 : (p.M + 255) / 256;
     hipError_t e;
     if (xf32 && p.x_ws) {
         EMB_CHECK_ARG(aligned16(p.x_ws), "x_bf16_workspace must be 16-byte aligned");
@@ -501,23 +529,7 @@ int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
         p.ldx = p.K;
         xf32 = false;
     }
-    if (xf32) {
-        switch (mode) {
-            case Y_BF16: e = launch<true, Y_BF16>(p, stream); break;
-            case Y_F32_ROUNDED: e = launch<true, Y_F32_ROUNDED>(p, stream); break;
-            case Y_F32_RAW: e = launch<true, Y_F32_RAW>(p, stream); break;
-            case Y_GATED: e = launch<true, Y_GATED>(p, stream); break;
-            default: e = launch<true, Y_QKV>(p, stream); break;
-        }
-    } else {
-        switch (mode) {
-            case Y_BF16: e = launch<false, Y_BF16>(p, stream); break;
-            case Y_F32_ROUNDED: e = launch<false, Y_F32_ROUNDED>(p, stream); break;
-            case Y_F32_RAW: e = launch<false, Y_F32_RAW>(p, stream); break;
-            case Y_GATED: e = launch<false, Y_GATED>(p, stream); break;
-            default: e = launch<false, Y_QKV>(p, stream); break;
-        }
-    }
+    e = narrow ? dispatch<128>(p, xf32, mode, stream) : dispatch<256>(p, xf32, mode, stream);
     if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "w8a16 launch: %s", hipGetErrorString(e));
     return EMB_OK;
 }

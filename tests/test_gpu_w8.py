@@ -172,18 +172,20 @@ def test_w8_reference_named_faces(emb, orc, torch_dev):
                                       K // 16, N * 4, 2, N, None) == -1
 
 
-def test_w8_qkv_append_matches_gemm(emb, orc, torch_dev):
+@pytest.mark.parametrize("M,K,n_q,hkv,d,cap", [
+    (70, 128, 256, 2, 64, 128),          # a narrow grid: 128-row tiles
+    (1030, 128, 4608, 8, 128, 1280),     # 5 x 52 tiles of 256 rows fill the chip: 256-row tiles
+])
+def test_w8_qkv_append_matches_gemm(emb, orc, torch_dev, M, K, n_q, hkv, d, cap):
     """The fused projection writes exactly the plain GEMM's bf16 values: Q into
     its buffer, K/V into the pool rows of slots[m] through a permuted block
     table; skipped slots (-1, >= capacity, unmapped page) leave the pool as is."""
     torch, dev = torch_dev
-    rng = np.random.default_rng(21)
-    M, K, n_q, hkv, d = 70, 128, 256, 2, 64
+    rng = np.random.default_rng(21 + M)
     n_kv = hkv * d
     N = n_q + 2 * n_kv
     w, q, s, s_st = _weights(orc, rng, K, N)
     x = orc.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
-    cap = 128
     n_pages = cap // 16
     bt = rng.permutation(n_pages + 3)[:n_pages].astype(np.int32)
     bt[5] = -1  # one unmapped page
@@ -227,3 +229,21 @@ def test_w8_config5_shape_sampled_rows(emb, orc, torch_dev):
                             *rng.integers(0, M, 8).tolist()}), np.int64)
     _, yf_ref = orc.w8a16_gemm(x, q, s_st, M, K, N, rows=rows)
     assert_close(yf[rows], yf_ref, "w8 config-5 rows")
+
+
+def test_w8_tile_heights_agree(emb, orc, torch_dev):
+    """A grid that fills the chip runs 256-row tiles, a narrow one 128-row
+    tiles; every output element sums the same k-steps in the same order
+    either way, so the first rows of a wide GEMM (256-row tiles) equal the same
+    rows computed alone (a narrow grid) bit for bit."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(23)
+    M, K, N = 1030, 256, 6656  # 5 x 52 tiles of 256 rows
+    w, q, s, s_st = _weights(orc, rng, K, N)
+    x = orc.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    wide = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_F32_RAW)
+    part = _gemm(emb, torch, dev, np.ascontiguousarray(x[:300]), q, s_st, 300, K, N, emb.EMB_W8_Y_F32_RAW)
+    assert np.array_equal(wide[:300], part)
+    rows = np.array([0, 127, 128, 255, 256, 299, 512, 1029], np.int64)
+    _, yf_ref = orc.w8a16_gemm(x, q, s_st, M, K, N, rows=rows)
+    assert_close(wide[rows], yf_ref, "w8 wide rows")
