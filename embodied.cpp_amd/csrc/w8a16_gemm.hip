@@ -26,10 +26,10 @@
 // two operands agree and no byte of W is moved twice.
 //
 // Tiling.  A workgroup of 4 waves (2 x 2) computes a 256 x 128 tile of y; a
-// wave owns 128 x 64 (4 x 2 MFMA blocks, 128 accumulator registers).  When
-// 256-row tiles would leave CUs idle (fewer tiles than CUs) the tiles are
-// 128 x 128 instead (2 x 2 blocks a wave); each output element sums the same
-// k-steps in the same order either way.  K moves
+// wave owns 128 x 64 (4 x 2 MFMA blocks, 128 accumulator registers).  Where
+// 256-row tiles would need no fewer rounds of resident workgroups, the tiles
+// are 128 x 128 instead (2 x 2 blocks a wave); each output element sums the
+// same k-steps in the same order either way.  K moves
 // in tiles of 64.  The next k-tile's x and W words are loaded into registers
 // while the current one is multiplied; they are then converted (x: permuted;
 // W: u8 -> bf16(u8 - 128), once per workgroup) and written to the single LDS
@@ -510,11 +510,16 @@ int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
     EMB_CHECK_ARG(p.ldx >= p.K && (p.ldx * (xf32 ? 4 : 2)) % 16 == 0, "x row stride must cover K, 16-byte aligned");
     EMB_CHECK_ARG(aligned16(p.x) && aligned16(p.qw), "x and qweight must be 16-byte aligned");
     EMB_CHECK_ARG((int64_t)p.M * (p.N / 64) < INT_MAX, "problem too large");
-    // 256-row tiles, unless they leave CUs idle (fewer tiles than the 256 CUs,
-    // e.g. the 3072-wide O-projection over 1560 rows: 168 tiles); then
-    // 128-row tiles, twice as many, each half the work
+    // Tile height by rounds of resident workgroups on MI355X's 256 CUs: two
+    // 256-row workgroups fit a CU (VGPRs), three 128-row ones.  A 128-row
+    // tile costs about 0.77 of a 256-row one (its B-tile dequant is not
+    // halved), so 128-row tiles win unless they need more rounds (measured:
+    // 1560 x 3072 -> 3072 and 3200 x 4096 -> 6144 run faster with 128 rows,
+    // 1560 x 3072 -> 9216 with 256).
     p.n_tiles = (p.N + BN - 1) / BN;
-    const bool narrow = (int64_t)((p.M + 255) / 256) * p.n_tiles < 256;
+    const int64_t rounds256 = ((int64_t)((p.M + 255) / 256) * p.n_tiles + 511) / 512;
+    const int64_t rounds128 = ((int64_t)((p.M + 127) / 128) * p.n_tiles + 767) / 768;
+    const bool narrow = rounds128 <= rounds256;
     p.m_tiles = narrow ? (p.M + 127) / 128 : (p.M + 255) / 256;
     hipError_t e;
     if (xf32 && p.x_ws) {

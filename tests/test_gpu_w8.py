@@ -173,8 +173,8 @@ def test_w8_reference_named_faces(emb, orc, torch_dev):
 
 
 @pytest.mark.parametrize("M,K,n_q,hkv,d,cap", [
-    (70, 128, 256, 2, 64, 128),          # a narrow grid: 128-row tiles
-    (1030, 128, 4608, 8, 128, 1280),     # 5 x 52 tiles of 256 rows fill the chip: 256-row tiles
+    (70, 128, 256, 2, 64, 128),          # a small grid: 128-row tiles
+    (1560, 128, 3072, 24, 128, 1600),    # the config-5 width: 256-row tiles (one round; 128 rows need two)
 ])
 def test_w8_qkv_append_matches_gemm(emb, orc, torch_dev, M, K, n_q, hkv, d, cap):
     """The fused projection writes exactly the plain GEMM's bf16 values: Q into
@@ -232,18 +232,18 @@ def test_w8_config5_shape_sampled_rows(emb, orc, torch_dev):
 
 
 def test_w8_tile_heights_agree(emb, orc, torch_dev):
-    """A grid that fills the chip runs 256-row tiles, a narrow one 128-row
-    tiles; every output element sums the same k-steps in the same order
-    either way, so the first rows of a wide GEMM (256-row tiles) equal the same
-    rows computed alone (a narrow grid) bit for bit."""
+    """1560 x 9216 runs 256-row tiles (one round; 128-row tiles would need
+    two), 300 rows of it alone run 128-row tiles; every output element sums
+    the same k-steps in the same order either way, so the two agree bit for
+    bit."""
     torch, dev = torch_dev
     rng = np.random.default_rng(23)
-    M, K, N = 1030, 256, 6656  # 5 x 52 tiles of 256 rows
+    M, K, N = 1560, 256, 9216
     w, q, s, s_st = _weights(orc, rng, K, N)
     x = orc.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
     wide = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_F32_RAW)
     part = _gemm(emb, torch, dev, np.ascontiguousarray(x[:300]), q, s_st, 300, K, N, emb.EMB_W8_Y_F32_RAW)
     assert np.array_equal(wide[:300], part)
-    rows = np.array([0, 127, 128, 255, 256, 299, 512, 1029], np.int64)
+    rows = np.array([0, 127, 128, 255, 256, 299, 512, 1535, 1536, 1559], np.int64)
     _, yf_ref = orc.w8a16_gemm(x, q, s_st, M, K, N, rows=rows)
     assert_close(wide[rows], yf_ref, "w8 wide rows")
