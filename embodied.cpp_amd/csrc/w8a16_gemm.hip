@@ -632,6 +632,16 @@ int emb_w8a16_gated_residual(const void *x, int32_t x_is_f32, int64_t ldx, const
                       !overlaps(gate_bias, (int64_t)N * 4),
                   "out overlaps gate or bias");
     EMB_CHECK_ARG(residual != out || ldr == ldo, "in-place update needs ldr == ldo");
+    if (x_is_f32 && x_bf16_workspace) {  // the workspace is written before the GEMM reads the others
+        const char *w0 = (const char *)x_bf16_workspace, *w1 = w0 + (int64_t)M * K * 2;
+        auto hits = [&](const void *q, int64_t bytes) {
+            return q && (const char *)q < w1 && w0 < (const char *)q + bytes;
+        };
+        EMB_CHECK_ARG(!hits(out, ((int64_t)(M - 1) * ldo + N) * 4) && !hits(residual, ((int64_t)(M - 1) * ldr + N) * 4) &&
+                          !hits(gate, gate ? ((int64_t)(M - 1) * ldg + N) * 4 : 0) && !hits(bias, (int64_t)N * 4) &&
+                          !hits(gate_bias, (int64_t)N * 4) && !hits(x, ((int64_t)(M - 1) * ldx + K) * 4),
+                      "x_bf16_workspace overlaps an input or out");
+    }
     GParams p{};
     p.x = x;
     p.ldx = ldx;

@@ -185,6 +185,10 @@ def test_device_entry_points_reject_bad_arguments(emb):
     assert G(buf, 0, 128, buf, buf, 4, 128, 128, None, r, 64, None, r, 128, o, 128, 0, None) == -1
     assert "ldg" in emb.last_error()
     assert G(buf, 0, 96, buf, buf, 4, 96, 96, None, None, 96, None, r, 96, o, 96, 0, None) == -4
+    # an f32 x workspace that overlaps out is refused
+    assert L.emb_w8a16_gated_residual(buf, 1, 128, buf, buf, 4, 128, 128, None, None, 128, None, r, 128, o, 128, 0,
+                                      C.c_void_p((1 << 20) + 256), None) == -1
+    assert "workspace overlaps" in emb.last_error()
     assert L.emb_kv_gather(buf, buf, buf, 0, None, 16, buf, buf, 1, 128, None) == -1
     assert L.lingbot_runtime_kv_update_f32(buf, buf, buf, buf, buf, 4, 1, 64, 4, None) == -1
     assert "capacity" in emb.last_error()
