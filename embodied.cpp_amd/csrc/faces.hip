@@ -356,11 +356,8 @@ int flex_common(const float *q, const float *k, const float *v, const int *row_p
 // 1/sqrt(head_dim), causal (key j visible to query i iff j <= i) or full, and
 // the output rounded to bf16 values.  K/V are staged into identity-paged pools
 // (with the f16 shadow) and the paged attention runs: the causal mask is the
-// chunk mask with chunk 1.
-__global__ __launch_bounds__(256) void round_bf16_kernel(float *__restrict__ y, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        y[i] = __builtin_bit_cast(float, (uint32_t)to_bf16(y[i]) << 16);
-}
+// chunk mask with chunk 1, and the rounding is done by the attention's own
+// output stores (out_bf16_round).
 
 int cosmos3_gqa(const float *q, const float *k, const float *v, float *y, int n_q, int n_kv, int hidden, int kv,
                 int q_heads, int kv_heads, int head_dim, bool causal, hipStream_t stream) {
@@ -413,6 +410,7 @@ int cosmos3_gqa(const float *q, const float *k, const float *v, float *y, int n_
         a.chunk = 1;
         a.window = -1;
     }
+    a.out_bf16_round = 1;  // the reference rounds its output to bf16 values
     if ((rc = emb_paged_attention(&a, stream))) return rc;
     if (pl.stage_out) {
         const int64_t total = (int64_t)n_q * q_heads * head_dim;
@@ -421,9 +419,7 @@ int cosmos3_gqa(const float *q, const float *k, const float *v, float *y, int n_
                            (int64_t)head_dim * 4, (int64_t)hidden * 4, (int64_t)0);
         if ((rc = launch_check("scatter_out"))) return rc;
     }
-    const int64_t n = (int64_t)n_q * hidden;
-    hipLaunchKernelGGL(round_bf16_kernel, dim3(grid_for(n)), dim3(256), 0, stream, y, n);
-    return launch_check("round_bf16");
+    return EMB_OK;
 }
 
 int ggml_type_ok(int32_t t) { return t == EMB_GGML_F32 || t == EMB_GGML_F16 || t == EMB_GGML_BF16; }

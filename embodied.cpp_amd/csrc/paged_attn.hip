@@ -115,6 +115,7 @@ struct KParams {
     const void *q;
     float *out;
     int64_t q_stride, out_stride;
+    int32_t round_out;  // store every output value rounded to bf16 precision
     const int32_t *cu_q;
     const int32_t *n_keys;
     const int32_t *q_pos0;
@@ -173,6 +174,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     uint32_t u = __builtin_bit_cast(uint32_t, f);
     u += 0x7fffu + ((u >> 16) & 1u);
     return u >> 16;
+}
+
+// The four values rounded to bf16 precision (nearest even), kept as f32.
+__device__ __forceinline__ f32x4 round_bf16x4(const f32x4 &v) {
+    return f32x4{__builtin_bit_cast(float, f32_to_bf16_bits(v[0]) << 16),
+                 __builtin_bit_cast(float, f32_to_bf16_bits(v[1]) << 16),
+                 __builtin_bit_cast(float, f32_to_bf16_bits(v[2]) << 16),
+                 __builtin_bit_cast(float, f32_to_bf16_bits(v[3]) << 16)};
 }
 
 // Two bf16 (packed in a dword) -> two f16 (packed in a dword), round to nearest even.
@@ -1049,7 +1058,7 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
                 for (int u = 1; u < RPI; ++u) off = sub == u ? cand[u] : off;
             }
             if (off < 0) continue;
-            *reinterpret_cast<f32x4 *>(p.out + off + c * 4) = rv[i];
+            *reinterpret_cast<f32x4 *>(p.out + off + c * 4) = p.round_out ? round_bf16x4(rv[i]) : rv[i];
         }
     } else {
         if (!row_ok) return;
@@ -1060,7 +1069,7 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
             for (int j = 0; j < 4; ++j) {
                 const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
                                  acc_o[dt][j * 4 + 3] * sc};
-                *reinterpret_cast<f32x4 *>(p.out + off + dt * 32 + j * 8 + lhi * 4) = v;
+                *reinterpret_cast<f32x4 *>(p.out + off + dt * 32 + j * 8 + lhi * 4) = p.round_out ? round_bf16x4(v) : v;
             }
     }
 }
@@ -1135,7 +1144,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     o[e] += wgt[s] * (float)__builtin_bit_cast(_Float16, (uint16_t)(os[s][j][e >> 1] >> ((e & 1) * 16)));
-            *reinterpret_cast<f32x4 *>(dst + j * 8) = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+            const f32x4 r = {o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+            *reinterpret_cast<f32x4 *>(dst + j * 8) = p.round_out ? round_bf16x4(r) : r;
         }
     }
 }
@@ -1231,6 +1241,7 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     kp.out = a->out;
     kp.q_stride = a->q_stride;
     kp.out_stride = a->out_stride;
+    kp.round_out = a->out_bf16_round != 0;
     kp.cu_q = a->cu_q;
     kp.n_keys = a->n_keys;
     kp.q_pos0 = a->q_pos0;

@@ -42,6 +42,7 @@ class AttnArgs(C.Structure):
         ("block_map_batch_stride", C.c_int64),
         ("splits", C.c_int32), ("workspace", vp),
         ("n_keys_uniform", C.c_int32),
+        ("out_bf16_round", C.c_int32),
     ]
 
 
@@ -451,7 +452,7 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
                     valid_stride=0, mask_kind=EMB_MASK_FULL, chunk=0, window=-1, mask=None,
                     mask_q_stride=0, mask_batch_stride=0, block_map=None, block_size=0,
                     block_map_cols=0, block_map_batch_stride=0, splits=1, workspace=None,
-                    n_keys_uniform=0, stream=None):
+                    n_keys_uniform=0, out_bf16_round=False, stream=None):
     a = AttnArgs()
     a.q = ptr(q); a.q_is_f32 = int(q_is_f32)
     a.q_stride = q_stride if q_stride is not None else hq * d
@@ -467,6 +468,7 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
     a.block_map = ptr(block_map); a.block_size = block_size; a.block_map_cols = block_map_cols
     a.block_map_batch_stride = block_map_batch_stride
     a.splits = splits; a.workspace = ptr(workspace); a.n_keys_uniform = n_keys_uniform
+    a.out_bf16_round = int(out_bf16_round)
     return check(lib().emb_paged_attention(C.byref(a), stream_ptr(stream)), "emb_paged_attention")
 
 

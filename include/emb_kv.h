@@ -303,6 +303,9 @@ typedef struct emb_attn_args {
     int32_t splits;
     void *workspace;
     int32_t n_keys_uniform;            /* keys per sequence when cu_q and n_keys are NULL */
+    int32_t out_bf16_round;            /* nonzero: every output value is stored rounded to
+                                          bf16 precision (nearest even), still as f32 -- the
+                                          Cosmos3 kernels' output rounding, done in the store */
 } emb_attn_args;
 
 size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_t hkv,

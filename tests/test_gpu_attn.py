@@ -128,6 +128,22 @@ def test_uniform_batch_form(emb, orc, torch_dev):
             assert_close(uni[b], s.oracle(orc, b, 1 / 16), f"uniform seq {b} splits {splits}")
 
 
+@pytest.mark.parametrize("d,hq,hkv", [(256, 8, 1), (128, 4, 2), (64, 2, 2)])
+def test_out_bf16_round(emb, orc, torch_dev, d, hq, hkv):
+    """out_bf16_round stores every output value rounded to bf16 (nearest even):
+    exactly the rounding of the unrounded output, through both output paths
+    (staged through LDS at D = 256, direct below) and through the split-K merge."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0011 + d)
+    s = Seqs(orc, rng, [300, 77], [40, 13], hq, hkv, d)
+    for splits in (1, 3):
+        plain = s.run(emb, torch, dev, 1 / math.sqrt(d), splits=splits)
+        rnd = s.run(emb, torch, dev, 1 / math.sqrt(d), splits=splits, out_bf16_round=True)
+        for b in range(2):
+            want = orc.bf16_to_f32(orc.f32_to_bf16(np.ascontiguousarray(plain[b])))
+            assert np.array_equal(rnd[b], want), f"d {d} splits {splits} seq {b}"
+
+
 def test_multi_session_sweep(emb, orc, torch_dev):
     """cfg4: sessions with prefix lengths U[300,1200] + 51 queries, pages scattered in one pool."""
     torch, dev = torch_dev
