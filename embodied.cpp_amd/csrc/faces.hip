@@ -99,13 +99,6 @@ __global__ __launch_bounds__(256) void stage_kv_kernel(StageGeom g, uint16_t *__
     }
 }
 
-// The block tables of `batch` sequences that share one staged K/V set
-// (kv_batch == 1: every table is the identity over pages [0, pps)).
-__global__ void tables_kernel(int32_t *__restrict__ bt, int32_t pps, int32_t batch) {
-    const int32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < batch * pps) bt[i] = i % pps;
-}
-
 // Queries to bf16 [batch][n_q][heads][dp], dims past d_src zero.
 __global__ __launch_bounds__(256) void stage_q_kernel(Src4 q, int32_t n_q, int32_t heads, int32_t d_src, int32_t dp,
                                                      int32_t batch, uint16_t *__restrict__ out) {
@@ -222,12 +215,10 @@ int stage_kv(const Plan &pl, const Src4 &k, const Src4 &v, char *ws, hipStream_t
     hipLaunchKernelGGL(stage_kv_kernel, dim3(grid_for(total)), dim3(256), 0, stream, g, (uint16_t *)(ws + pl.off_k),
                        (uint16_t *)(ws + pl.off_v), (uint16_t *)(ws + pl.off_v16), (int32_t *)(ws + pl.off_bt));
     int rc = launch_check("stage_kv");
-    if (rc) return rc;
-    if (pl.kv_batch != 1) return EMB_OK;  // stage_kv_kernel wrote one table per sequence
-    const int32_t n = pl.batch * pl.pps;
-    hipLaunchKernelGGL(tables_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, (int32_t *)(ws + pl.off_bt), pl.pps,
-                       pl.batch);
-    return launch_check("tables");
+    // kv_batch > 1: stage_kv_kernel wrote one table per sequence; kv_batch == 1:
+    // every sequence reads the same identity-paged K/V, which the attention
+    // takes as NULL block tables (page = slot / 16), so no table is written
+    return rc;
 }
 
 void base_args(const Plan &pl, char *ws, float scale, emb_attn_args &a) {
@@ -238,8 +229,9 @@ void base_args(const Plan &pl, char *ws, float scale, emb_attn_args &a) {
     a.k_pool = ws + pl.off_k;
     a.v_pool = ws + pl.off_v;
     a.v16_pool = ws + pl.off_v16;
-    a.block_tables = (const int32_t *)(ws + pl.off_bt);
-    a.bt_stride = pl.pps;
+    // shared K/V (kv_batch == 1): identity pages, no tables (see stage_kv)
+    a.block_tables = pl.kv_batch == 1 ? nullptr : (const int32_t *)(ws + pl.off_bt);
+    a.bt_stride = pl.kv_batch == 1 ? 0 : pl.pps;
     a.capacity = pl.pps * 16;
     a.batch = pl.batch;
     a.hq = pl.hq;

@@ -144,6 +144,48 @@ def test_out_bf16_round(emb, orc, torch_dev, d, hq, hkv):
             assert np.array_equal(rnd[b], want), f"d {d} splits {splits} seq {b}"
 
 
+@pytest.mark.parametrize("d,hq,hkv,mask", [(256, 8, 1, "full"), (128, 8, 2, "chunk"), (64, 4, 4, "full")])
+def test_null_block_tables_are_identity(emb, orc, torch_dev, d, hq, hkv, mask):
+    """NULL block tables map slot s to page s / 16 (the faces pass them for
+    K/V shared by every sequence): bit-identical to explicit identity tables,
+    for two sequences over the same pages, split-K 1 and 3, and within the bar
+    of the oracle."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0012 + d)
+    nk, nq, B = 300, 40, 2
+    pages = (nk + 15) // 16
+    k = orc.f32_to_bf16(rng.standard_normal((nk, hkv, d)).astype(np.float32))
+    v = orc.f32_to_bf16(rng.standard_normal((nk, hkv, d)).astype(np.float32))
+    q = orc.f32_to_bf16(rng.standard_normal((B * nq, hq, d)).astype(np.float32))
+    kp = np.zeros(pages * hkv * 16 * d, np.uint16)
+    vp = np.zeros_like(kp)
+    orc.paged_append(k.reshape(nk, -1), v.reshape(nk, -1), hkv * d, np.arange(nk, dtype=np.int32),
+                     np.arange(pages, dtype=np.int32), hkv, d, pages * 16, kp, vp)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16) if a.dtype == np.uint16 else a).to(dev)
+    kpt, vpt, v16 = t(kp), t(vp), t(v16_shadow(vp, d))
+    kw = dict(chunk=16, window=-1, mask_kind=emb.EMB_MASK_CHUNK) if mask == "chunk" else {}
+    outs = {}
+    for splits in (1, 3):
+        ws = None
+        if splits > 1:
+            ws = torch.empty(emb.attn_workspace_bytes(B, nq, hq, hkv, d, splits) // 4 + 4, dtype=torch.float32,
+                             device=dev)
+        for how in ("tables", "null"):
+            out = torch.full((B * nq, hq, d), float("nan"), dtype=torch.float32, device=dev)
+            bt = t(np.tile(np.arange(pages, dtype=np.int32), B)) if how == "tables" else None
+            emb.paged_attention(q=t(q), out=out, k_pool=kpt, v_pool=vpt, v16_pool=v16, batch=B, hq=hq, hkv=hkv, d=d,
+                                max_q=nq, scale=1 / math.sqrt(d), capacity=pages * 16, n_keys_uniform=nk,
+                                block_tables=bt, bt_stride=pages if bt is not None else 0, splits=splits,
+                                workspace=ws, **kw)
+            torch.cuda.synchronize()
+            outs[(splits, how)] = out.cpu().numpy()
+        assert np.array_equal(outs[(splits, "tables")], outs[(splits, "null")]), f"splits {splits}"
+    okw = dict(chunk=16, window=-1) if mask == "chunk" else {}
+    for b in range(B):
+        ref = orc.gqa_attention(q[b * nq:(b + 1) * nq], k, v, nq, nk, hq, hkv, d, 1 / math.sqrt(d), **okw)
+        assert_close(outs[(1, "null")][b * nq:(b + 1) * nq], ref, f"null tables seq {b}")
+
+
 def test_multi_session_sweep(emb, orc, torch_dev):
     """cfg4: sessions with prefix lengths U[300,1200] + 51 queries, pages scattered in one pool."""
     torch, dev = torch_dev
