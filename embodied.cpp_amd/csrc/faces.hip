@@ -61,41 +61,54 @@ struct StageGeom {
     int32_t kv_batch;                           // 1 (shared by every sequence) or batch
 };
 
-// One thread per (sequence b, slot t of the sequence's pages, head h, dim d):
-// K and V as bf16 at their page positions, V also as f16 in the shadow order.
-// Slots past n_kv and dims past d_src are written as zeros.  The sequence's
-// block table (identity pages b*pps + i) is written alongside.
+// One thread per (sequence b, slot t of the sequence's pages, head h, 8-dim
+// chunk c), slots fastest: K and V as bf16 at their page positions (K as one
+// 16-byte store of the chunk; the 16 slots of a page write each V page row of
+// 32 bytes together), V also as f16 in the shadow order.  Slots past n_kv and
+// dims past d_src are written as zeros.  The sequence's block table (identity
+// pages b*pps + i) is written alongside.
 __global__ __launch_bounds__(256) void stage_kv_kernel(StageGeom g, uint16_t *__restrict__ k_pool,
                                                       uint16_t *__restrict__ v_pool, uint16_t *__restrict__ v16_pool,
                                                       int32_t *__restrict__ bt) {
-    const int64_t slots = (int64_t)g.pps * 16;
-    const int64_t total = (int64_t)g.kv_batch * slots * g.heads * g.dp;
+    const int32_t CH = g.dp / 8;
+    const int64_t total = (int64_t)g.kv_batch * g.pps * 16 * g.heads * CH;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * blockDim.x) {
         const int32_t t = (int32_t)(idx % 16);
         int64_t r = idx / 16;
-        const int32_t d = (int32_t)(r % g.dp);
-        r /= g.dp;
+        const int32_t c = (int32_t)(r % CH);
+        r /= CH;
         const int32_t h = (int32_t)(r % g.heads);
         r /= g.heads;
         const int32_t pg = (int32_t)(r % g.pps);
         const int32_t b = (int32_t)(r / g.pps);
         const int32_t j = pg * 16 + t;
-        float kf = 0.0f, vf = 0.0f;
-        if (j < g.n_kv && d < g.d_src) {
-            kf = load_elem(g.k.base + d * g.k.nb0 + j * g.k.nb1 + h * g.k.nb2 + b * g.k.nb3, g.k.type);
-            vf = load_elem(g.v.base + d * g.v.nb0 + j * g.v.nb1 + h * g.v.nb2 + b * g.v.nb3, g.v.type);
+        float kf[8], vf[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int32_t d = c * 8 + e;
+            kf[e] = vf[e] = 0.0f;
+            if (j < g.n_kv && d < g.d_src) {
+                kf[e] = load_elem(g.k.base + d * g.k.nb0 + j * g.k.nb1 + h * g.k.nb2 + b * g.k.nb3, g.k.type);
+                vf[e] = load_elem(g.v.base + d * g.v.nb0 + j * g.v.nb1 + h * g.v.nb2 + b * g.v.nb3, g.v.type);
+            }
         }
         const int64_t page = (int64_t)b * g.pps + pg;
         const int64_t pbase = (page * g.heads + h) * 16 * g.dp;
-        k_pool[pbase + t * g.dp + d] = to_bf16(kf);
-        const uint16_t vb = to_bf16(vf);
-        v_pool[pbase + d * 16 + t] = vb;
-        // the shadow holds f16 of the value as given (exact for f16 sources)
-        v16_pool[pbase + emb::v16_index(d, t)] =
-            __builtin_bit_cast(uint16_t, g.v.type == EMB_GGML_F16 ? (_Float16)vf
-                                                                  : (_Float16)__builtin_bit_cast(float, (uint32_t)vb << 16));
-        if (h == 0 && d == 0 && t == 0) bt[page] = (int32_t)page;
+        uint32_t kw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kw[e] = (uint32_t)to_bf16(kf[2 * e]) | ((uint32_t)to_bf16(kf[2 * e + 1]) << 16);
+        *reinterpret_cast<uint4 *>(k_pool + pbase + (int64_t)t * g.dp + c * 8) = uint4{kw[0], kw[1], kw[2], kw[3]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int32_t d = c * 8 + e;
+            const uint16_t vb = to_bf16(vf[e]);
+            v_pool[pbase + d * 16 + t] = vb;
+            // the shadow holds f16 of the value as given (exact for f16 sources)
+            v16_pool[pbase + emb::v16_index(d, t)] = __builtin_bit_cast(
+                uint16_t, g.v.type == EMB_GGML_F16 ? (_Float16)vf[e] : (_Float16)__builtin_bit_cast(float, (uint32_t)vb << 16));
+        }
+        if (h == 0 && c == 0 && t == 0) bt[page] = (int32_t)page;
     }
 }
 
@@ -211,7 +224,7 @@ struct Plan {
 
 int stage_kv(const Plan &pl, const Src4 &k, const Src4 &v, char *ws, hipStream_t stream) {
     StageGeom g{k, v, pl.n_kv, pl.hkv, pl.d_src, pl.dp, pl.batch, pl.pps, pl.kv_batch};
-    const int64_t total = (int64_t)pl.kv_batch * pl.pps * 16 * pl.hkv * pl.dp;
+    const int64_t total = (int64_t)pl.kv_batch * pl.pps * 16 * pl.hkv * (pl.dp / 8);
     hipLaunchKernelGGL(stage_kv_kernel, dim3(grid_for(total)), dim3(256), 0, stream, g, (uint16_t *)(ws + pl.off_k),
                        (uint16_t *)(ws + pl.off_v), (uint16_t *)(ws + pl.off_v16), (int32_t *)(ws + pl.off_bt));
     int rc = launch_check("stage_kv");
