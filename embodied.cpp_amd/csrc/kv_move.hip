@@ -11,9 +11,10 @@
 // V is stored transposed inside each page so that the attention kernel reads 16
 // consecutive keys of one dimension with one 32-byte access.
 //
-// Both kernels are byte movers bound by HBM.  Threads are ordered with the
+// The kernels are byte movers bound by HBM.  Threads are ordered with the
 // token index fastest, so the 16 tokens of one page write (append) or read
-// (gather) one 32-byte V row together, while the K rows move as 16-byte vectors.
+// (gather) one 32-byte V row together, while the K rows move as 16-byte vectors;
+// large appends read and write whole head rows and turn V through LDS.
 #include <hip/hip_runtime.h>
 
 #include "emb_common.h"
@@ -112,6 +113,62 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const Src *__restrict__ 
     }
 }
 
+// Large appends: a workgroup per (16 consecutive tokens, head).  Each token's
+// head row is read whole (chunk fastest: D*2 contiguous bytes, against 16 bytes
+// per row with the token-fastest order) and its K row written whole; V goes
+// through LDS and is written token-fastest, so the 16 tokens of a page (with
+// consecutive slots) still write each 32-byte V row together.  Same skip rules
+// and the same values as kv_append_kernel.
+constexpr int ROWS_MAX_D = 256;
+
+template <typename Src>
+__global__ __launch_bounds__(256) void kv_append_rows_kernel(const Src *__restrict__ k, const Src *__restrict__ v,
+                                                             const int32_t *__restrict__ slots,
+                                                             const int32_t *__restrict__ block_table,
+                                                             uint16_t *__restrict__ k_pool,
+                                                             uint16_t *__restrict__ v_pool,
+                                                             uint16_t *__restrict__ v16_pool, MoveGeom g) {
+    // V of the 16 tokens, [token][d] with rows of D + 8 (16-byte aligned rows;
+    // the 16 tokens of one d fall in 16 different banks)
+    __shared__ __attribute__((aligned(16))) uint16_t vt[16 * (ROWS_MAX_D + 8)];
+    const int32_t ld = g.head_dim + 8;
+    const int32_t h = (int32_t)(blockIdx.x % g.heads);
+    const int32_t s0 = (int32_t)(blockIdx.x / g.heads) * 16;
+    for (int32_t u = threadIdx.x; u < 16 * g.chunks; u += 256) {
+        const int32_t tok = u / g.chunks, c = u % g.chunks;
+        const int32_t s = s0 + tok;
+        if (s >= g.n) continue;
+        const int64_t src = (int64_t)s * g.src_stride + h * g.head_dim + c * 8;
+        uint16_t kv[8], vv[8];
+        load8<Src>(k + src, kv);
+        load8<Src>(v + src, vv);
+        *reinterpret_cast<u32x4 *>(vt + tok * ld + c * 8) = pack8(vv);
+        const int32_t slot = slots[s];
+        if (slot < 0 || slot >= g.capacity) continue;
+        const int32_t page = block_table ? block_table[slot >> 4] : (slot >> 4);
+        if (page < 0) continue;
+        const int64_t pbase = ((int64_t)page * g.heads + h) * 16 * g.head_dim;
+        *reinterpret_cast<u32x4 *>(k_pool + pbase + (slot & 15) * g.head_dim + c * 8) = pack8(kv);
+    }
+    __syncthreads();
+    for (int32_t w = threadIdx.x; w < 16 * g.head_dim; w += 256) {
+        const int32_t tok = w % 16, d = w / 16;
+        const int32_t s = s0 + tok;
+        if (s >= g.n) continue;
+        const int32_t slot = slots[s];
+        if (slot < 0 || slot >= g.capacity) continue;
+        const int32_t page = block_table ? block_table[slot >> 4] : (slot >> 4);
+        if (page < 0) continue;
+        const int32_t t = slot & 15;
+        const int64_t pbase = ((int64_t)page * g.heads + h) * 16 * g.head_dim;
+        const uint16_t b = vt[tok * ld + d];
+        v_pool[pbase + d * 16 + t] = b;
+        if (v16_pool)
+            v16_pool[pbase + emb::v16_index(d, t)] =
+                __builtin_bit_cast(uint16_t, (_Float16)__builtin_bit_cast(float, (uint32_t)b << 16));
+    }
+}
+
 // One thread per (key i, head h, chunk c), i fastest.  Dst = uint16_t (bf16)
 // or float (the f32 face).
 template <typename Dst>
@@ -175,8 +232,15 @@ int launch_append(const Src *k, const Src *v, int64_t src_stride, int32_t n, con
     MoveGeom g{n, heads, head_dim, head_dim / 8, capacity, src_stride};
     const int64_t total = (int64_t)n * heads * g.chunks;
     EMB_CHECK_ARG(total < INT32_MAX, "append too large for one launch");
-    hipLaunchKernelGGL(kv_append_kernel<Src>, dim3(grid_for(total)), dim3(256), 0, stream, k, v, slots,
-                       block_table, (uint16_t *)k_pool, (uint16_t *)v_pool, (uint16_t *)v16_pool, g);
+    const int64_t groups = ((int64_t)n + 15) / 16 * heads;
+    if (n >= 256 && head_dim <= ROWS_MAX_D && groups < INT32_MAX) {
+        // enough tokens for a workgroup per (16 tokens, head) to fill the chip
+        hipLaunchKernelGGL(kv_append_rows_kernel<Src>, dim3((unsigned)groups), dim3(256), 0, stream, k, v, slots,
+                           block_table, (uint16_t *)k_pool, (uint16_t *)v_pool, (uint16_t *)v16_pool, g);
+    } else {
+        hipLaunchKernelGGL(kv_append_kernel<Src>, dim3(grid_for(total)), dim3(256), 0, stream, k, v, slots,
+                           block_table, (uint16_t *)k_pool, (uint16_t *)v_pool, (uint16_t *)v16_pool, g);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "kv_append launch: %s", hipGetErrorString(e));
     return EMB_OK;

@@ -30,11 +30,13 @@ def _np(t):
     return a.view(np.uint16) if a.dtype == np.int16 else a
 
 
-@pytest.mark.parametrize("H,D,extra", [(24, 128, 0), (1, 256, 64), (2, 64, 8)])
-def test_append_gather_bit_exact(emb, orc, torch_dev, H, D, extra):
+@pytest.mark.parametrize("H,D,extra,n", [(24, 128, 0, 120), (1, 256, 64, 120), (2, 64, 8, 120),
+                                         # 256 tokens and more: a workgroup per (16 tokens, head)
+                                         (24, 128, 0, 700), (1, 256, 64, 300), (3, 64, 8, 517)])
+def test_append_gather_bit_exact(emb, orc, torch_dev, H, D, extra, n):
     torch, dev = torch_dev
-    rng = np.random.default_rng(H * 1000 + D)
-    cap, n = 200, 120
+    rng = np.random.default_rng(H * 1000 + D + n)
+    cap = max(200, n + 80)
     n_pages_seq = (cap + 15) // 16
     pool_pages = n_pages_seq + 7
     bt = rng.permutation(pool_pages)[:n_pages_seq].astype(np.int32)
@@ -117,10 +119,11 @@ def test_chunk_eviction_sequence_bit_exact(emb, orc, torch_dev):
         assert np.array_equal(_np(gk), ok) and np.array_equal(_np(gv), ov), step
 
 
-def test_reference_named_f32_update_gather(emb, orc, torch_dev):
+@pytest.mark.parametrize("cap,n", [(50, 30), (400, 300)])  # 300 tokens: the (16 tokens, head) workgroups
+def test_reference_named_f32_update_gather(emb, orc, torch_dev, cap, n):
     torch, dev = torch_dev
-    H, D, cap, n = 3, 64, 50, 30
-    rng = np.random.default_rng(2)
+    H, D = 3, 64
+    rng = np.random.default_rng(2 + n)
     kb = orc.f32_to_bf16(rng.standard_normal((n, H, D)).astype(np.float32))
     vb = orc.f32_to_bf16(rng.standard_normal((n, H, D)).astype(np.float32))
     kf, vf = orc.bf16_to_f32(kb), orc.bf16_to_f32(vb)
