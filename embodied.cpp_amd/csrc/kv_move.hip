@@ -233,8 +233,10 @@ int launch_append(const Src *k, const Src *v, int64_t src_stride, int32_t n, con
     const int64_t total = (int64_t)n * heads * g.chunks;
     EMB_CHECK_ARG(total < INT32_MAX, "append too large for one launch");
     const int64_t groups = ((int64_t)n + 15) / 16 * heads;
-    if (n >= 256 && head_dim <= ROWS_MAX_D && groups < INT32_MAX) {
-        // enough tokens for a workgroup per (16 tokens, head) to fill the chip
+    if (groups >= 1024 && head_dim <= ROWS_MAX_D && groups < INT32_MAX) {
+        // enough (16 tokens, head) workgroups to fill the chip (4 a CU); fewer,
+        // larger ones would leave a small append (a pi0.5 step: 918 tokens of
+        // one head, 58 workgroups) latency-bound
         hipLaunchKernelGGL(kv_append_rows_kernel<Src>, dim3((unsigned)groups), dim3(256), 0, stream, k, v, slots,
                            block_table, (uint16_t *)k_pool, (uint16_t *)v_pool, (uint16_t *)v16_pool, g);
     } else {

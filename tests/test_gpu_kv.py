@@ -31,8 +31,8 @@ def _np(t):
 
 
 @pytest.mark.parametrize("H,D,extra,n", [(24, 128, 0, 120), (1, 256, 64, 120), (2, 64, 8, 120),
-                                         # 256 tokens and more: a workgroup per (16 tokens, head)
-                                         (24, 128, 0, 700), (1, 256, 64, 300), (3, 64, 8, 517)])
+                                         # 1024 (16 tokens, head) groups and more: a workgroup each
+                                         (24, 128, 0, 700), (8, 256, 64, 2048), (16, 64, 8, 1030)])
 def test_append_gather_bit_exact(emb, orc, torch_dev, H, D, extra, n):
     torch, dev = torch_dev
     rng = np.random.default_rng(H * 1000 + D + n)
@@ -119,7 +119,7 @@ def test_chunk_eviction_sequence_bit_exact(emb, orc, torch_dev):
         assert np.array_equal(_np(gk), ok) and np.array_equal(_np(gv), ov), step
 
 
-@pytest.mark.parametrize("cap,n", [(50, 30), (400, 300)])  # 300 tokens: the (16 tokens, head) workgroups
+@pytest.mark.parametrize("cap,n", [(50, 30), (5600, 5500)])  # 5500 tokens: the (16 tokens, head) workgroups
 def test_reference_named_f32_update_gather(emb, orc, torch_dev, cap, n):
     torch, dev = torch_dev
     H, D = 3, 64
