@@ -233,10 +233,12 @@ int launch_append(const Src *k, const Src *v, int64_t src_stride, int32_t n, con
     const int64_t total = (int64_t)n * heads * g.chunks;
     EMB_CHECK_ARG(total < INT32_MAX, "append too large for one launch");
     const int64_t groups = ((int64_t)n + 15) / 16 * heads;
-    if (groups >= 1024 && head_dim <= ROWS_MAX_D && groups < INT32_MAX) {
-        // enough (16 tokens, head) workgroups to fill the chip (4 a CU); fewer,
-        // larger ones would leave a small append (a pi0.5 step: 918 tokens of
-        // one head, 58 workgroups) latency-bound
+    if (groups >= 768 && head_dim <= ROWS_MAX_D && groups < INT32_MAX) {
+        // enough (16 tokens, head) workgroups to fill the chip (3 a CU).
+        // Measured: 1560 x 24 heads x 128 (2352 groups) 20.6 -> 13.2 us and
+        // 14688 x 1 x 256 (918) 18.2 -> 12.7 us on this path, while
+        // 1040 x 8 x 256 (520 groups) is slower on it (10.9 against 8.4 us) and
+        // the pi0.5 step's 918 x 1 x 256 (58 groups) is latency-bound
         hipLaunchKernelGGL(kv_append_rows_kernel<Src>, dim3((unsigned)groups), dim3(256), 0, stream, k, v, slots,
                            block_table, (uint16_t *)k_pool, (uint16_t *)v_pool, (uint16_t *)v16_pool, g);
     } else {
