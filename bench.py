@@ -413,6 +413,13 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
     set_split(best)
     ms_step, _ = c.time_graph(lambda st: [layer(l, st) for l in range(n_layers)], max(2, steps // 4), 1)
     ms_attn, _ = c.time_graph(lambda st: [layer(l, st, False) for l in range(n_layers)], max(2, steps // 4), 1)
+    # the chunk append alone (1560 tokens x 24 heads into the evicted chunk's
+    # slots, with the f16 shadow), 30 layers' pools in one graph
+    ms_app, _ = c.time_graph(lambda st: [emb.kv_append(knew, vnew, H * d, C, new_slots, pools[l][3], cap, pools[l][0],
+                                                       pools[l][1], H, d, stream=st, v16_pool=pools[l][2])
+                                         for l in range(n_layers)], max(2, steps // 4), 1)
+    app_us = ms_app * 1e3 / n_layers
+    app_bytes = C * H * d * 2 * 2 + C * H * d * 2 * 3 + C * 4  # read K, V; write K, V, shadow; slots
     fl_layer = 4.0 * C * H * cap * d
     attn_layer_us = ms_attn * 1e3 / n_layers
     del pools
@@ -420,7 +427,8 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
     return dict(ms_per_step=ms_step, attn_ms_per_step=ms_attn, attn_us_per_layer=attn_layer_us,
                 attn_tflops=fl_layer / (attn_layer_us * 1e-6) / 1e12,
                 mfma_frac=fl_layer / (attn_layer_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS,
-                flops_per_layer=fl_layer, layers=n_layers, splits=best, split_sweep_us_per_layer=sweep)
+                flops_per_layer=fl_layer, layers=n_layers, splits=best, split_sweep_us_per_layer=sweep,
+                append_chunk_us=app_us, append_chunk_gbs=app_bytes / (app_us * 1e-6) / 1e9)
 
 
 def bench_meta(c: Ctx, steps, n_layers=30):
