@@ -254,3 +254,18 @@ def test_gated_residual_wrapper_refuses_short_buffers(emb):
     with pytest.raises(ValueError, match="gate"):  # a gate view at column 5N has too few columns left
         emb.w8a16_gated_residual(x, torch.zeros((K // 16, 4 * N), dtype=torch.int32), s, M, K, N, r, r,
                                  gate=tp[:, 5 * N + 1:], ldg=6 * N)
+
+
+def test_reference_f32_faces_reject_like_the_reference(emb):
+    """lingbot_runtime_kv_update_f32 / _gather_f32 return -1 for a null pointer
+    or a non-positive seq, n_heads, head_dim or capacity, before any launch, as
+    the reference's wrappers do (kernels/lingbot/lingbot_flex_attn_cuda.cu:911-913,
+    :998-1001)."""
+    L = emb.lib()
+    b = C.c_void_p(256)
+    U, G = L.lingbot_runtime_kv_update_f32, L.lingbot_runtime_kv_gather_f32
+    for seq, h, d, cap in [(0, 2, 64, 64), (4, 0, 64, 64), (4, 2, 0, 64), (4, 2, 64, 0), (-1, 2, 64, 64)]:
+        assert U(b, b, b, b, b, seq, h, d, cap, None) == -1
+        assert G(b, b, b, b, b, seq, h, d, cap, None) == -1
+    assert U(None, b, b, b, b, 4, 2, 64, 64, None) == -1
+    assert G(b, b, None, b, b, 4, 2, 64, 64, None) == -1
