@@ -419,6 +419,17 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
                                                        pools[l][1], H, d, stream=st, v16_pool=pools[l][2])
                                          for l in range(n_layers)], max(2, steps // 4), 1)
     app_us = ms_app * 1e3 / n_layers
+    # the compact copy of all 14040 cached rows in valid-slot order that the
+    # reference makes before its attention (runtime_kv_gather); the paged
+    # attention reads the pages in place instead
+    gk = torch.empty((cap, H, d), dtype=torch.int16, device=c.dev)
+    gv = torch.empty_like(gk)
+    valid_all = c.i32(np.arange(cap, dtype=np.int32))
+    ms_g, _ = c.time_graph(lambda st: [emb.kv_gather(pools[l][0], pools[l][1], valid_all, cap, pools[l][3], cap, gk,
+                                                     gv, H, d, stream=st) for l in range(4)], max(2, steps // 4), 1)
+    gather_us = ms_g * 1e3 / 4
+    gather_bytes = cap * H * d * 2 * 4 + cap * 4  # read K, V; write K, V; the slot list
+    del gk, gv
     app_bytes = C * H * d * 2 * 2 + C * H * d * 2 * 3 + C * 4  # read K, V; write K, V, shadow; slots
     fl_layer = 4.0 * C * H * cap * d
     attn_layer_us = ms_attn * 1e3 / n_layers
@@ -428,7 +439,8 @@ def bench_cfg3(c: Ctx, steps, warmup, n_layers=30, eager_only=False):
                 attn_tflops=fl_layer / (attn_layer_us * 1e-6) / 1e12,
                 mfma_frac=fl_layer / (attn_layer_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS,
                 flops_per_layer=fl_layer, layers=n_layers, splits=best, split_sweep_us_per_layer=sweep,
-                append_chunk_us=app_us, append_chunk_gbs=app_bytes / (app_us * 1e-6) / 1e9)
+                append_chunk_us=app_us, append_chunk_gbs=app_bytes / (app_us * 1e-6) / 1e9,
+                gather_window_us=gather_us, gather_window_gbs=gather_bytes / (gather_us * 1e-6) / 1e9)
 
 
 def bench_meta(c: Ctx, steps, n_layers=30):

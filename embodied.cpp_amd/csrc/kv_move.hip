@@ -250,6 +250,56 @@ int launch_append(const Src *k, const Src *v, int64_t src_stride, int32_t n, con
     return EMB_OK;
 }
 
+// Large gathers: the append's row layout in reverse -- a workgroup per (16
+// consecutive output rows, head) reads V token-fastest (the 16 keys of a page
+// with consecutive slots read one 32-byte V row together) into LDS, and writes
+// each output row's K and V whole.  Same skip rules and values as
+// kv_gather_kernel.
+template <typename Dst>
+__global__ __launch_bounds__(256) void kv_gather_rows_kernel(const uint16_t *__restrict__ k_pool,
+                                                             const uint16_t *__restrict__ v_pool,
+                                                             const int32_t *__restrict__ valid,
+                                                             const int32_t *__restrict__ block_table,
+                                                             Dst *__restrict__ k_out, Dst *__restrict__ v_out,
+                                                             MoveGeom g) {
+    __shared__ __attribute__((aligned(16))) uint16_t vt[16 * (ROWS_MAX_D + 8)];
+    const int32_t ld = g.head_dim + 8;
+    const int32_t h = (int32_t)(blockIdx.x % g.heads);
+    const int32_t i0 = (int32_t)(blockIdx.x / g.heads) * 16;
+    for (int32_t w = threadIdx.x; w < 16 * g.head_dim; w += 256) {
+        const int32_t tok = w % 16, d = w / 16, i = i0 + tok;
+        if (i >= g.n) continue;
+        const int32_t slot = valid[i];
+        if (slot < 0 || slot >= g.capacity) continue;
+        const int32_t page = block_table ? block_table[slot >> 4] : (slot >> 4);
+        if (page < 0) continue;
+        vt[tok * ld + d] = v_pool[(((int64_t)page * g.heads + h) * g.head_dim + d) * 16 + (slot & 15)];
+    }
+    __syncthreads();
+    for (int32_t u = threadIdx.x; u < 16 * g.chunks; u += 256) {
+        const int32_t tok = u / g.chunks, c = u % g.chunks, i = i0 + tok;
+        if (i >= g.n) continue;
+        const int32_t slot = valid[i];
+        if (slot < 0 || slot >= g.capacity) continue;
+        const int32_t page = block_table ? block_table[slot >> 4] : (slot >> 4);
+        if (page < 0) continue;
+        uint16_t kv[8], vv[8];
+        load8<uint16_t>(k_pool + (((int64_t)page * g.heads + h) * 16 + (slot & 15)) * g.head_dim + c * 8, kv);
+        load8<uint16_t>(vt + tok * ld + c * 8, vv);
+        const int64_t dst = ((int64_t)i * g.heads + h) * g.head_dim + c * 8;
+        if constexpr (sizeof(Dst) == 2) {
+            *reinterpret_cast<u32x4 *>(k_out + dst) = pack8(kv);
+            *reinterpret_cast<u32x4 *>(v_out + dst) = pack8(vv);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                k_out[dst + e] = __builtin_bit_cast(float, (uint32_t)kv[e] << 16);
+                v_out[dst + e] = __builtin_bit_cast(float, (uint32_t)vv[e] << 16);
+            }
+        }
+    }
+}
+
 template <typename Dst>
 int launch_gather(const void *k_pool, const void *v_pool, const int32_t *valid, int32_t n,
                   const int32_t *block_table, int32_t capacity, Dst *k_out, Dst *v_out, int32_t heads,
@@ -261,8 +311,14 @@ int launch_gather(const void *k_pool, const void *v_pool, const int32_t *valid, 
                   "buffers must be 16-byte aligned");
     MoveGeom g{n, heads, head_dim, head_dim / 8, capacity, 0};
     const int64_t total = (int64_t)n * heads * g.chunks;
-    hipLaunchKernelGGL(kv_gather_kernel<Dst>, dim3(grid_for(total)), dim3(256), 0, stream,
-                       (const uint16_t *)k_pool, (const uint16_t *)v_pool, valid, block_table, k_out, v_out, g);
+    const int64_t groups = ((int64_t)n + 15) / 16 * heads;
+    if (groups >= 768 && head_dim <= ROWS_MAX_D && groups < INT32_MAX) {  // the append's rule
+        hipLaunchKernelGGL(kv_gather_rows_kernel<Dst>, dim3((unsigned)groups), dim3(256), 0, stream,
+                           (const uint16_t *)k_pool, (const uint16_t *)v_pool, valid, block_table, k_out, v_out, g);
+    } else {
+        hipLaunchKernelGGL(kv_gather_kernel<Dst>, dim3(grid_for(total)), dim3(256), 0, stream,
+                           (const uint16_t *)k_pool, (const uint16_t *)v_pool, valid, block_table, k_out, v_out, g);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "kv_gather launch: %s", hipGetErrorString(e));
     return EMB_OK;
