@@ -39,7 +39,8 @@ def v16_shadow(v_pool: np.ndarray, d: int) -> np.ndarray:
     include/emb_kv.h specifies it: row t of dim d at position P = t with bits 2
     and 3 swapped, the two 8-key halves exchanged when bit 3 of d is set."""
     v = v_pool.reshape(-1, d, 16)
-    f = (v.astype(np.uint32) << 16).view(np.float32).astype(np.float16).view(np.uint16)
+    with np.errstate(over="ignore", invalid="ignore"):  # random bit patterns: out of f16 range is inf, as on the GPU
+        f = (v.astype(np.uint32) << 16).view(np.float32).astype(np.float16).view(np.uint16)
     t = np.arange(16)
     P = (t & 3) | ((t >> 1) & 4) | ((t << 1) & 8)
     dd = np.arange(d)[:, None]
