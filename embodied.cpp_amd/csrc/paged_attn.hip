@@ -80,6 +80,9 @@ constexpr int WAVES = 4;
 constexpr int ROWS_PER_WAVE = 32;
 constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
 constexpr float RESCALE_TH = 8.0f;  // log2 units
+// A row whose largest |O| lies below this (with a non-empty key set) is
+// recomputed exactly from the bf16 pool (see the epilogue).
+constexpr float EXACT_TINY = 0x1p-12f;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int SEG_PAGES = 1024;  // block-table entries held in LDS at a time (16384 keys)
 // Block-table entries every wave of the DMA path holds in registers from the start.
@@ -145,7 +148,7 @@ struct KParams {
     // 32-row block in the MFMA accumulator order (element ((c*64 + lane)*4 + e)
     // of a block is dims c*8 + (lane/32)*4 + e of row lane%32)
     uint16_t *ws_o;
-    float *ws_ml;    // [batch*hkv][splits][row_tiles*128][2]: m (log2 units), l
+    float *ws_ml;    // [batch*hkv][splits][row_tiles*128][4]: m (log2 units), l, k (O/l stored as O/l * 2^-k), 0
 };
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
@@ -977,28 +980,170 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
         l_run = a + c;
     }
 
+    // Exactness.  V reaches the loop's P.V product as f16, which is exact
+    // only for |v| in [2^-14, 65504]: a larger value turns the row into
+    // inf/NaN, and when every visible value is far below 2^-14 the f16
+    // subnormals lose the row's precision.  A wave any of whose rows ended
+    // non-finite, or with a largest |O| below 2^-12 over a non-empty key set
+    // (|O| <= max |v|, so all its weight sat on values the f16 path cannot
+    // hold), recomputes its rows here from the bf16 pool: K and V read
+    // straight into the MFMA operands, P in f32 split into two bf16 parts
+    // (P_hi + P_lo carries 16 bits), P.V as two bf16 MFMAs.  No LDS, no
+    // barrier: the other waves of the workgroup go on to the epilogue.
+    if (wave_live) {
+        float amax = 0.0f;
+        bool fin = true;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                fin = fin && __builtin_isfinite(acc_o[dt][e]);
+                amax = fmaxf(amax, fabsf(acc_o[dt][e]));
+            }
+        float a, c;
+        half_pair(amax, a, c);
+        amax = fmaxf(a, c);
+        const bool bad = row_ok && l_run > 0.0f && (!fin || amax < EXACT_TINY * l_run);
+        if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+            // the query fragment again (reloaded rather than kept live past the
+            // loop, where it would cost the loop registers)
+            load_q();
+            pin_q();
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i) acc_o[i] = f32x16{};
+            float m_x = -INFINITY, l_x = 0.0f;
+            // logical slot of key j (-1: a zero row), and its page
+            auto slot_of = [&](int32_t j) {
+                int32_t sl;
+                if constexpr (VALID) {
+                    sl = j < nk ? valid_b[j] : -1;
+                    if (sl >= p.capacity) sl = -1;
+                } else {
+                    sl = j < lim ? j : -1;
+                }
+                if (sl >= 0 && bt_b && (sl >> 4) >= p.bt_stride) sl = -1;
+                return sl;
+            };
+            auto page_row = [&](int32_t sl) -> int32_t {  // (page, kv head) index of slot sl, or -1
+                if (sl < 0) return -1;
+                const int32_t page = page_of(bt_b, sl);
+                return page < 0 ? -1 : page * p.hkv + kvh;
+            };
+            for (int32_t t = t_lo; t < t_hi; ++t) {
+                const int32_t k0 = t * G::KT;
+                f32x16 sx[G::KB];
+#pragma unroll
+                for (int kb = 0; kb < G::KB; ++kb) {
+                    const int32_t sl = slot_of(k0 + kb * 32 + lrow);
+                    const int32_t pr = page_row(sl);
+                    const uint16_t *krow = p.k_pool + ((int64_t)(pr < 0 ? 0 : pr) * 16 + (sl & 15)) * D + lhi * 8;
+                    sx[kb] = f32x16{};
+#pragma unroll
+                    for (int kk = 0; kk < D / 16; ++kk) {
+                        u32x4 w = {0u, 0u, 0u, 0u};
+                        if (pr >= 0) w = *reinterpret_cast<const u32x4 *>(krow + kk * 16);
+                        sx[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), qf[kk], sx[kb],
+                                                                         0, 0, 0);
+                    }
+                }
+                apply_mask(sx, k0);
+                const float m_new = fmaxf(m_x, tile_max(sx));
+                const float alpha = m_x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_x - m_new) * p.c_log2);
+#pragma unroll
+                for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
+                l_x *= alpha;
+                m_x = m_new;
+                const float neg = m_new == -INFINITY ? 0.0f : -m_new * p.c_log2;
+#pragma unroll
+                for (int kb = 0; kb < G::KB; ++kb) {
+                    // k-step ks of the block: lane holds S elements 8ks..8ks+7,
+                    // keys 16ks + (m/4)*8 + lhi*4 + m%4 (m = 0..7); V supplies
+                    // the same keys for dim dt*32 + lrow.
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        u32x4 ph, pl;
+#pragma unroll
+                        for (int m = 0; m < 8; m += 2) {
+                            uint32_t h[2], lo[2];
+#pragma unroll
+                            for (int u = 0; u < 2; ++u) {
+                                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sx[kb][ks * 8 + m + u], p.c_log2, neg));
+                                l_x += pv;
+                                h[u] = f32_to_bf16_bits(pv);
+                                lo[u] = f32_to_bf16_bits(pv - bf16_to_f32(h[u]));
+                            }
+                            ph[m / 2] = h[0] | (h[1] << 16);
+                            pl[m / 2] = lo[0] | (lo[1] << 16);
+                        }
+                        int32_t vs[8], vr[8];
+#pragma unroll
+                        for (int m = 0; m < 8; ++m) {
+                            vs[m] = slot_of(k0 + kb * 32 + ks * 16 + (m >> 2) * 8 + lhi * 4 + (m & 3));
+                            vr[m] = page_row(vs[m]);
+                        }
+#pragma unroll
+                        for (int dt = 0; dt < D / 32; ++dt) {
+                            const int d = dt * 32 + lrow;
+                            u32x4 vw;
+#pragma unroll
+                            for (int m = 0; m < 8; m += 2) {
+                                uint32_t e0 = 0u, e1 = 0u;
+                                if (vr[m] >= 0) e0 = p.v_pool[((int64_t)vr[m] * D + d) * 16 + (vs[m] & 15)];
+                                if (vr[m + 1] >= 0) e1 = p.v_pool[((int64_t)vr[m + 1] * D + d) * 16 + (vs[m + 1] & 15)];
+                                vw[m / 2] = e0 | (e1 << 16);
+                            }
+                            acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                __builtin_bit_cast(bf16x8, vw), __builtin_bit_cast(bf16x8, ph), acc_o[dt], 0, 0, 0);
+                            acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                __builtin_bit_cast(bf16x8, vw), __builtin_bit_cast(bf16x8, pl), acc_o[dt], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+            half_pair(l_x, a, c);
+            l_run = a + c;
+            m_run = m_x;
+        }
+    }
+
     const float sc = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    // Split partials: O / l in f16 (O/l of a split is a weighted mean of V
-    // rows, so f16 keeps 11 bits relative to each element; the merge
-    // reweights the splits by l) with (m, l) per row.  Only the merge kernel
-    // reads them, so each wave stores its 32-row block in the accumulator
-    // order: every store instruction writes 512 contiguous bytes, with no
-    // staging through LDS.  (Rows past the end carry values nothing reads.)
+    // Split partials: O / l in f16 with a per-row power-of-two scale 2^k that
+    // puts the row's largest |O/l| in [2^14, 2^15) (O/l of a split is a
+    // weighted mean of V rows, so f16 keeps 11 bits relative to the row's
+    // largest element, whatever its magnitude; the merge reweights the splits
+    // by l), and (m, l, k) per row.  Only the merge kernel reads them, so each
+    // wave stores its 32-row block in the accumulator order: every store
+    // instruction writes 512 contiguous bytes, with no staging through LDS.
+    // (Rows past the end carry values nothing reads.)
     if (p.splits > 1) {
         const int64_t unit_row0 = ((int64_t)(b * p.hkv + kvh) * p.splits + split) * ((int64_t)p.row_tiles * ROWS_PER_WG);
+        float omax = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) omax = fmaxf(omax, fabsf(acc_o[dt][e]));
+        {
+            float a, c;
+            half_pair(omax, a, c);
+            omax = fmaxf(a, c) * sc;
+        }
+        int ex = 0;
+        if (omax > 0.0f && __builtin_isfinite(omax)) frexpf(omax, &ex);
+        const int k = omax > 0.0f ? min(max(ex - 15, -100), 100) : 0;  // omax * 2^-k in [2^14, 2^15)
         if (row_ok && lhi == 0) {
             const int64_t rowi = unit_row0 + my_row;
-            *reinterpret_cast<float2 *>(p.ws_ml + rowi * 2) =
-                float2{m_run == -INFINITY ? -INFINITY : m_run * p.c_log2, l_run};
+            *reinterpret_cast<f32x4 *>(p.ws_ml + rowi * 4) =
+                f32x4{m_run == -INFINITY ? -INFINITY : m_run * p.c_log2, l_run, (float)k, 0.0f};
         }
         if (wave_live) {
+            const float scs = ldexpf(sc, -k);
             uint16_t *blk = p.ws_o + (unit_row0 + row0 + wave * ROWS_PER_WAVE) * D + lane * 4;
 #pragma unroll
             for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
-                                     acc_o[dt][j * 4 + 3] * sc};
+                    const f32x4 v = {acc_o[dt][j * 4] * scs, acc_o[dt][j * 4 + 1] * scs, acc_o[dt][j * 4 + 2] * scs,
+                                     acc_o[dt][j * 4 + 3] * scs};
                     *reinterpret_cast<u32x2 *>(blk + (dt * 4 + j) * 256) = f16x4_bits(v);
                 }
         }
@@ -1106,18 +1251,21 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
         const int64_t rows_per_unit = (int64_t)blocks_per_unit * 32;
         const int64_t unit0 = (int64_t)(b * p.hkv + kvh) * p.splits;
         float ms[MS], ls[MS];
+        int ks[MS];
         u32x2 os[MS][NCH];
 #pragma unroll
         for (int s = 0; s < MS; ++s) {
             ms[s] = -INFINITY;
             ls[s] = 0.0f;
+            ks[s] = 0;
 #pragma unroll
             for (int j = 0; j < NCH; ++j) os[s][j] = u32x2{0u, 0u};
             if (s < p.splits) {
                 const int64_t u = (unit0 + s) * rows_per_unit;
-                const float2 ml = *reinterpret_cast<const float2 *>(p.ws_ml + (u + row) * 2);
-                ms[s] = ml.x;
-                ls[s] = ml.y;
+                const f32x4 ml = *reinterpret_cast<const f32x4 *>(p.ws_ml + (u + row) * 4);
+                ms[s] = ml[0];
+                ls[s] = ml[1];
+                ks[s] = (int)ml[2];
                 const uint16_t *src = p.ws_o + (u + blk * 32) * D + (cg * NCH * 64 + lane) * 4;
 #pragma unroll
                 for (int j = 0; j < NCH; ++j) os[s][j] = *reinterpret_cast<const u32x2 *>(src + j * 256);
@@ -1133,6 +1281,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
             l += wgt[s];
         }
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int s = 0; s < MS; ++s) wgt[s] = ldexpf(wgt[s], ks[s]);  // the partial's stored scale
         const int32_t tok = row / p.G;
         const int32_t head = kvh * p.G + row % p.G;
         float *dst = p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + cg * NCH * 8 + (lane >> 5) * 4;
@@ -1335,7 +1485,7 @@ size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_
     if (batch <= 0 || max_q <= 0 || hq <= 0 || hkv <= 0 || hq % hkv || head_dim <= 0 || splits <= 1) return 0;
     const int64_t row_tiles = ((int64_t)max_q * (hq / hkv) + ROWS_PER_WG - 1) / ROWS_PER_WG;
     const int64_t rows_all = (int64_t)batch * hkv * splits * row_tiles * ROWS_PER_WG;
-    return (size_t)rows_all * ((size_t)head_dim * sizeof(uint16_t) + 2 * sizeof(float));
+    return (size_t)rows_all * ((size_t)head_dim * sizeof(uint16_t) + 4 * sizeof(float));
 }
 
 int emb_paged_attention(const emb_attn_args *a, hipStream_t stream) {

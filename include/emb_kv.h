@@ -26,6 +26,15 @@
  * given; attention given one copies its pages into LDS as they are.  The bf16
  * pool stays the bit-exact store (gather reads it).  A shadow must start
  * zero-filled (rows never appended are read, multiplied by zero weights).
+ *
+ * Value range.  Attention is exact for any finite bf16 V (the reference's
+ * f32 range): its fast P.V product takes V as f16 (from the shadow, or
+ * converted in registers), and a query row whose output comes out non-finite
+ * (some visible |v| > 65504) or whose largest |out| is below 2^-12 over a
+ * non-empty key set (its weight sits on values below f16's normal range) is
+ * recomputed by the kernel from the bf16 pool with a bf16 P.V product (P kept
+ * to 16 bits as two bf16 parts).  Split-K partials carry a per-row
+ * power-of-two scale, so they hold any finite magnitude too.
  */
 #ifndef EMB_KV_H
 #define EMB_KV_H
@@ -299,7 +308,9 @@ typedef struct emb_attn_args {
     int32_t block_size, block_map_cols;
     int64_t block_map_batch_stride;
     /* split-K over keys: 0/1 = none.  With splits > 1, workspace must hold
-     * emb_attn_workspace_bytes(...) bytes of device memory. */
+     * emb_attn_workspace_bytes(...) bytes of device memory: per row tile of
+     * 128 rows and split, the partial O/l (f16, row-scaled by 2^k) and
+     * (m, l, k, 0) as four floats. */
     int32_t splits;
     void *workspace;
     int32_t n_keys_uniform;            /* keys per sequence when cu_q and n_keys are NULL */
@@ -357,7 +368,8 @@ int lingbot_runtime_kv_attn_cublas_f32(const float *q, const float *cache_k,
  * (u8 [seq_q][seq_k], masked variant); out = softmax(scale q.k) v, 0 for a
  * row with no visible key.  q/k/v/out: f32 [seq][n_heads][head_dim], device.
  * A key block listed twice counts once (the reference would count it twice).
- * Q and K round to bf16, P and V to f16 (fp32 accumulation).  These two own a
+ * Q, K and V round to bf16 (fp32 accumulation; V of any finite magnitude: see
+ * "Value range" above).  These two own a
  * device workspace (hipMalloc when a call needs more than the last one,
  * kept until exit): the first call at a new size must not be under stream
  * capture, and calls on one device from several threads must not overlap. */

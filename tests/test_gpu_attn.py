@@ -38,7 +38,7 @@ def _bf16(orc, rng, shape):
 class Seqs:
     """A batch of sequences whose keys live in one shared, randomly permuted page pool."""
 
-    def __init__(self, orc, rng, n_keys, n_q, hq, hkv, d, extra_pages=5):
+    def __init__(self, orc, rng, n_keys, n_q, hq, hkv, d, extra_pages=5, v_scale=1.0):
         self.n_keys, self.n_q = list(n_keys), list(n_q)
         self.hq, self.hkv, self.d = hq, hkv, d
         pages = [(k + 15) // 16 for k in n_keys]
@@ -51,7 +51,9 @@ class Seqs:
             self.bt[b, :p] = perm[o:o + p]
             o += p
         self.k = [_bf16(orc, rng, (k, hkv, d)) for k in n_keys]
-        self.v = [_bf16(orc, rng, (k, hkv, d)) for k in n_keys]
+        # v_scale: a number, or a function of the key count giving per-key scales [k][1][1]
+        vsc = v_scale if callable(v_scale) else (lambda k: v_scale)
+        self.v = [orc.f32_to_bf16((rng.standard_normal((k, hkv, d)) * vsc(k)).astype(np.float32)) for k in n_keys]
         self.q = [_bf16(orc, rng, (q, hq, d)) for q in n_q]
         self.kp = rng.integers(0, 65536, total * hkv * 16 * d, dtype=np.uint16)  # garbage elsewhere
         self.vp = rng.integers(0, 65536, total * hkv * 16 * d, dtype=np.uint16)
@@ -92,6 +94,7 @@ class Seqs:
             torch.cuda.synchronize()
             outs.append(out.cpu().numpy())
         assert np.array_equal(outs[0], outs[1], equal_nan=True), "register and LDS-copy paths differ"
+        self.reg_out = [outs[0][self.cu_q[b]:self.cu_q[b + 1]] for b in range(len(self.n_q))]
         o = outs[1]
         return [o[self.cu_q[b]:self.cu_q[b + 1]] for b in range(len(self.n_q))]
 
@@ -112,6 +115,22 @@ def test_pi05_action_expert_shape(emb, orc, torch_dev):
     assert_close(got4, s.oracle(orc, 0, scale), "pi05 cfg1 split-K 4")
     got6 = s.run(emb, torch, dev, scale, splits=6)[0]
     assert_close(got6, s.oracle(orc, 0, scale), "pi05 cfg1 split-K 6")
+
+
+def test_pi05_register_path_against_oracle(emb, orc, torch_dev):
+    """cfg1 shape with a second, shorter sequence: the register-staged path (no
+    V shadow) and the shadow path, each against the oracle, with and without
+    split-K (5 splits leave the last split of the short sequence empty)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0010)
+    s = Seqs(orc, rng, [867, 300], [51, 40], 8, 1, 256)
+    scale = 1 / 16
+    for splits in (1, 3, 5):
+        got = s.run(emb, torch, dev, scale, splits=splits)
+        for b in range(2):
+            ref = s.oracle(orc, b, scale)
+            assert_close(got[b], ref, f"shadow path b={b} splits={splits}")
+            assert_close(s.reg_out[b], ref, f"register path b={b} splits={splits}")
 
 
 def test_uniform_batch_form(emb, orc, torch_dev):

@@ -31,7 +31,7 @@ def _np(t):
 
 
 @pytest.mark.parametrize("H,D,extra,n", [(24, 128, 0, 120), (1, 256, 64, 120), (2, 64, 8, 120),
-                                         # 1024 (16 tokens, head) groups and more: a workgroup each
+                                         # 768 (16 tokens, head) groups and more: a workgroup each
                                          (24, 128, 0, 700), (8, 256, 64, 2048), (16, 64, 8, 1030)])
 def test_append_gather_bit_exact(emb, orc, torch_dev, H, D, extra, n):
     torch, dev = torch_dev
@@ -144,3 +144,38 @@ def test_reference_named_f32_update_gather(emb, orc, torch_dev, cap, n):
     src = {int(s): i for i, s in enumerate(slots)}
     idx = [src[int(s)] for s in valid]
     assert np.array_equal(gk.cpu().numpy(), kf[idx]) and np.array_equal(gv.cpu().numpy(), vf[idx])
+
+
+def test_reference_named_f32_update_narrows_general_f32(emb, orc, torch_dev):
+    """lingbot_runtime_kv_update_f32 on general f32 K/V (not bf16-representable,
+    RNE ties included, large and tiny magnitudes): the cache holds bf16, so the
+    gather returns bf16_rne(x) widened to f32 -- bit-exact to that rounding, not
+    to the f32 input (the reference's own f32 cache would return x itself;
+    kernels/lingbot/lingbot_flex_attn_cuda.cu:626-649)."""
+    torch, dev = torch_dev
+    H, D, cap, n = 2, 64, 64, 48
+    rng = np.random.default_rng(91)
+    k = rng.standard_normal((n, H, D)).astype(np.float32)
+    v = (rng.standard_normal((n, H, D)) * np.float32(1e30)).astype(np.float32)
+    kb = k.view(np.uint32)
+    kb[0, 0, :8] = (kb[0, 0, :8] & 0xFFFE0000) | 0x8000  # exact halfway, even bf16 LSB: rounds down
+    kb[1, 0, :8] = (kb[1, 0, :8] & 0xFFFE0000) | 0x18000  # exact halfway, odd bf16 LSB: rounds up
+    v[2, 1, :4] = np.float32(1e-30)
+    v[3, 1, :4] = np.float32(-7.1e-7)
+    slots = np.arange(n, dtype=np.int32)
+    ck = torch.zeros(cap * H * D, dtype=torch.float32, device=dev)
+    cv = torch.zeros_like(ck)
+    L = emb.lib()
+    assert L.lingbot_runtime_kv_update_f32(_t(torch, dev, k).data_ptr(), _t(torch, dev, v).data_ptr(),
+                                           ck.data_ptr(), cv.data_ptr(), _t(torch, dev, slots).data_ptr(),
+                                           n, H, D, cap, None) == 0
+    gk = torch.zeros((n, H, D), dtype=torch.float32, device=dev)
+    gv = torch.zeros_like(gk)
+    assert L.lingbot_runtime_kv_gather_f32(ck.data_ptr(), cv.data_ptr(), _t(torch, dev, slots).data_ptr(),
+                                           gk.data_ptr(), gv.data_ptr(), n, H, D, cap, None) == 0
+    torch.cuda.synchronize()
+    want_k = orc.bf16_to_f32(orc.f32_to_bf16(k))
+    want_v = orc.bf16_to_f32(orc.f32_to_bf16(v))
+    assert np.array_equal(gk.cpu().numpy(), want_k)
+    assert np.array_equal(gv.cpu().numpy(), want_v)
+    assert not np.array_equal(want_k, k)  # the inputs really needed rounding

@@ -219,7 +219,7 @@ def test_device_entry_points_reject_bad_arguments(emb):
     assert L.emb_dev_cache_restore(C.byref(dc), None, 4, None) == -1
     assert L.emb_dev_cache_clear_pred(None, None) == -1
     # f16 partial rows (O/l) plus f32 (m, l) per row
-    assert emb.attn_workspace_bytes(1, 51, 8, 1, 256, 4) == 4 * 512 * (256 * 2 + 2 * 4)
+    assert emb.attn_workspace_bytes(1, 51, 8, 1, 256, 4) == 4 * 512 * (256 * 2 + 4 * 4)  # f16 O + (m, l, k, 0)
     # whole-tensor faces: null pointers, head sizes past 256, ggml descriptors
     assert L.lingbot_flex_attn_f32(None, buf, buf, buf, buf, buf, 8, 8, 2, 64, 4, 0.1, None) == -1
     assert L.lingbot_flex_attn_f32(buf, buf, buf, buf, buf, buf, 8, 8, 2, 320, 4, 0.1, None) == -4
