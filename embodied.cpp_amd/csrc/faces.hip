@@ -23,8 +23,6 @@
 
 #include <cmath>
 #include <cstdio>
-#include <mutex>
-#include <unordered_map>
 #include <vector>
 
 #include "emb_common.h"
@@ -255,32 +253,33 @@ void base_args(const Plan &pl, char *ws, float scale, emb_attn_args &a) {
     a.mask_kind = EMB_MASK_FULL;
 }
 
-// Library-owned workspace of the reference-named faces (whose signatures carry
-// none): one grow-only device buffer per device.
-std::mutex g_ws_mu;
-std::unordered_map<int, std::pair<void *, size_t>> g_ws;
-
-int face_workspace(size_t bytes, char **out) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "hipGetDevice failed");
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    auto &slot = g_ws[dev];
-    if (slot.second < bytes) {
-        if (slot.first) {
-            // work queued earlier may still read the old buffer
-            if (hipDeviceSynchronize() != hipSuccess || hipFree(slot.first) != hipSuccess)
-                return emb::set_error(EMB_ERR_LAUNCH, "releasing the face workspace failed");
-            slot = {nullptr, 0};
+// Device workspace of one face call: the caller's buffer when one is given and
+// large enough, else a stream-ordered allocation (hipMallocAsync) that is
+// released on the same stream once the call's launches are queued
+// (hipFreeAsync).  Calls on different streams never share memory, nothing
+// waits for the device, and a call captured into a graph holds its own
+// allocation there.
+struct CallWs {
+    char *ptr = nullptr;
+    bool owned = false;
+    hipStream_t stream = nullptr;
+    int acquire(size_t bytes, void *caller, size_t caller_bytes, hipStream_t s) {
+        stream = s;
+        if (caller && caller_bytes >= bytes && aligned16(caller)) {
+            ptr = (char *)caller;
+            return EMB_OK;
         }
-        const size_t want = bytes + bytes / 4;
         void *p = nullptr;
-        if (hipMalloc(&p, want) != hipSuccess)
-            return emb::set_error(EMB_ERR_CAPACITY, "face workspace: hipMalloc(%zu) failed", want);
-        slot = {p, want};
+        if (hipMallocAsync(&p, bytes, s) != hipSuccess)
+            return emb::set_error(EMB_ERR_CAPACITY, "face workspace: hipMallocAsync(%zu) failed", bytes);
+        ptr = (char *)p;
+        owned = true;
+        return EMB_OK;
     }
-    *out = (char *)slot.first;
-    return EMB_OK;
-}
+    ~CallWs() {
+        if (owned) (void)hipFreeAsync(ptr, stream);
+    }
+};
 
 int flex_common(const float *q, const float *k, const float *v, const int *row_ptr, const int *col_idx,
                 const unsigned char *token_mask, float *out, int seq_q, int seq_k, int n_heads, int head_dim,
@@ -304,9 +303,10 @@ int flex_common(const float *q, const float *k, const float *v, const int *row_p
     pl.q_blocks = (seq_q + block_size - 1) / block_size;
     pl.k_blocks = (seq_k + block_size - 1) / block_size;
     pl.layout();
-    char *ws = nullptr;
-    int rc = face_workspace(pl.total, &ws);
+    CallWs cw;
+    int rc = cw.acquire(pl.total, nullptr, 0, stream);
     if (rc) return rc;
+    char *ws = cw.ptr;
     const int64_t row = (int64_t)n_heads * head_dim * 4;
     const Src4 sk{(const char *)k, 4, row, (int64_t)head_dim * 4, 0, EMB_GGML_F32};
     const Src4 sv{(const char *)v, 4, row, (int64_t)head_dim * 4, 0, EMB_GGML_F32};
@@ -365,7 +365,8 @@ int flex_common(const float *q, const float *k, const float *v, const int *row_p
 // output stores (out_bf16_round).
 
 int cosmos3_gqa(const float *q, const float *k, const float *v, float *y, int n_q, int n_kv, int hidden, int kv,
-                int q_heads, int kv_heads, int head_dim, bool causal, hipStream_t stream) {
+                int q_heads, int kv_heads, int head_dim, bool causal, void *caller_ws, size_t caller_ws_bytes,
+                hipStream_t stream) {
     EMB_CHECK_ARG(q && k && v && y, "null pointer");
     EMB_CHECK_ARG(n_q > 0 && n_kv > 0 && hidden > 0 && kv > 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0,
                   "non-positive size");
@@ -386,9 +387,10 @@ int cosmos3_gqa(const float *q, const float *k, const float *v, float *y, int n_
     pl.stage_q = padded || !aligned16(q);
     pl.stage_out = padded || !aligned16(y);
     pl.layout();
-    char *ws = nullptr;
-    int rc = face_workspace(pl.total, &ws);
+    CallWs cw;
+    int rc = cw.acquire(pl.total, caller_ws, caller_ws_bytes, stream);
     if (rc) return rc;
+    char *ws = cw.ptr;
     const Src4 sk{(const char *)k, 4, (int64_t)kv * 4, (int64_t)head_dim * 4, 0, EMB_GGML_F32};
     const Src4 sv{(const char *)v, 4, (int64_t)kv * 4, (int64_t)head_dim * 4, 0, EMB_GGML_F32};
     if ((rc = stage_kv(pl, sk, sv, ws, stream))) return rc;
@@ -655,14 +657,53 @@ int emb_ggml_flash_attn_ext(const emb_ggml_tensor *q, const emb_ggml_tensor *k, 
 int cosmos3_qwen_causal_gqa_attention_f32(const float *q, const float *k, const float *v, float *y, int tokens,
                                           int hidden, int kv, int q_heads, int kv_heads, int head_dim,
                                           hipStream_t stream) {
-    return cosmos3_gqa(q, k, v, y, tokens, tokens, hidden, kv, q_heads, kv_heads, head_dim, true, stream);
+    return cosmos3_gqa(q, k, v, y, tokens, tokens, hidden, kv, q_heads, kv_heads, head_dim, true, nullptr, 0,
+                       stream);
 }
 
 int cosmos3_qwen_gen_full_gqa_attention_f32(const float *q_gen, const float *k_all, const float *v_all, float *y_gen,
                                             int gen_tokens, int all_tokens, int hidden, int kv, int q_heads,
                                             int kv_heads, int head_dim, hipStream_t stream) {
     return cosmos3_gqa(q_gen, k_all, v_all, y_gen, gen_tokens, all_tokens, hidden, kv, q_heads, kv_heads, head_dim,
-                       false, stream);
+                       false, nullptr, 0, stream);
+}
+
+// The generated-token faces the Cosmos3 MoT denoise calls
+// (models/cosmos3.cpp:7889, :8187), with the caller's workspaces sized as the
+// model sizes them (:7221-7227): scores_workspace holds gen_tokens *
+// all_tokens * (q_heads / kv_heads) floats, bf16_workspace gen_tokens *
+// hidden + 2 * all_tokens * kv halfwords.  The staged K/V pools (K and V
+// bf16, the f16 V shadow) go into whichever of them is large enough (at the
+// model's shapes both are); only a shape whose workspaces are both too small
+// takes a stream-ordered allocation instead.  Same arithmetic as
+// cosmos3_qwen_gen_full_gqa_attention_f32; returns -1 for a null pointer or
+// inconsistent sizes, as the reference does (:1152-1158).
+int cosmos3_qwen_gen_full_gqa_attention_workspace_f32(const float *q_gen, const float *k_all, const float *v_all,
+                                                      float *y_gen, float *scores_workspace, int gen_tokens,
+                                                      int all_tokens, int hidden, int kv, int q_heads, int kv_heads,
+                                                      int head_dim, hipStream_t stream) {
+    EMB_CHECK_ARG(scores_workspace, "null scores_workspace");
+    EMB_CHECK_ARG(gen_tokens > 0 && all_tokens > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
+                  "non-positive size");
+    const size_t sbytes = (size_t)gen_tokens * all_tokens * (q_heads / kv_heads) * sizeof(float);
+    return cosmos3_gqa(q_gen, k_all, v_all, y_gen, gen_tokens, all_tokens, hidden, kv, q_heads, kv_heads, head_dim,
+                       false, scores_workspace, sbytes, stream);
+}
+
+int cosmos3_qwen_gen_full_gqa_attention_workspace_bf16tc_f32(const float *q_gen, const float *k_all,
+                                                             const float *v_all, float *y_gen, float *scores_workspace,
+                                                             unsigned short *bf16_workspace, int gen_tokens,
+                                                             int all_tokens, int hidden, int kv, int q_heads,
+                                                             int kv_heads, int head_dim, hipStream_t stream) {
+    EMB_CHECK_ARG(scores_workspace && bf16_workspace, "null workspace");
+    EMB_CHECK_ARG(gen_tokens > 0 && all_tokens > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 &&
+                      hidden > 0 && kv > 0,
+                  "non-positive size");
+    const size_t sbytes = (size_t)gen_tokens * all_tokens * (q_heads / kv_heads) * sizeof(float);
+    const size_t bbytes = ((size_t)gen_tokens * hidden + 2 * (size_t)all_tokens * kv) * sizeof(uint16_t);
+    void *ws = sbytes >= bbytes ? (void *)scores_workspace : (void *)bf16_workspace;
+    return cosmos3_gqa(q_gen, k_all, v_all, y_gen, gen_tokens, all_tokens, hidden, kv, q_heads, kv_heads, head_dim,
+                       false, ws, sbytes >= bbytes ? sbytes : bbytes, stream);
 }
 
 }  // extern "C"

@@ -126,6 +126,8 @@ _SIGS = {
     "lingbot_flex_attn_cuda_smoke": (C.c_int, [vp]),
     "cosmos3_qwen_causal_gqa_attention_f32": (C.c_int, [vp, vp, vp, vp] + [C.c_int] * 6 + [vp]),
     "cosmos3_qwen_gen_full_gqa_attention_f32": (C.c_int, [vp, vp, vp, vp] + [C.c_int] * 7 + [vp]),
+    "cosmos3_qwen_gen_full_gqa_attention_workspace_f32": (C.c_int, [vp, vp, vp, vp, vp] + [C.c_int] * 7 + [vp]),
+    "cosmos3_qwen_gen_full_gqa_attention_workspace_bf16tc_f32": (C.c_int, [vp] * 6 + [C.c_int] * 7 + [vp]),
     "emb_ggml_flash_attn_ext_workspace": (C.c_size_t, [C.POINTER(GgmlTensor)] * 5),
     "emb_ggml_flash_attn_ext": (C.c_int, [C.POINTER(GgmlTensor)] * 4 + [C.c_float] * 3 +
                                 [C.POINTER(GgmlTensor), vp, C.c_size_t, vp]),

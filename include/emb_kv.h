@@ -242,8 +242,9 @@ int emb_qkv_rownorm_rope_append(const float *qkv, int64_t ld, int32_t tokens, in
  * [tokens][kv], GQA (query head h reads kv head h / (q_heads / kv_heads)),
  * scale 1/sqrt(head_dim), output f32 rounded to bf16 values.  causal: key j
  * visible to query i iff j <= i; gen_full: every generated token sees all
- * all_tokens keys.  head_dim <= 256.  The first call at a new size allocates
- * the faces' grow-only workspace (not under stream capture). */
+ * all_tokens keys.  head_dim <= 256.  The K/V staging of the two faces
+ * without a workspace argument is a stream-ordered allocation of the call
+ * (hipMallocAsync, released by hipFreeAsync on the same stream). */
 int cosmos3_qwen_causal_gqa_attention_f32(const float *q, const float *k, const float *v, float *y,
                                           int tokens, int hidden, int kv, int q_heads, int kv_heads,
                                           int head_dim, hipStream_t stream);
@@ -251,6 +252,24 @@ int cosmos3_qwen_gen_full_gqa_attention_f32(const float *q_gen, const float *k_a
                                             float *y_gen, int gen_tokens, int all_tokens, int hidden,
                                             int kv, int q_heads, int kv_heads, int head_dim,
                                             hipStream_t stream);
+/* The generated-token faces the MoT denoise calls (models/cosmos3.cpp:7889,
+ * :8187; cosmos3_qwen_language_cuda.h:105-134), with caller workspaces sized
+ * as the model sizes them (:7221-7227): scores_workspace gen_tokens *
+ * all_tokens * (q_heads / kv_heads) floats, bf16_workspace gen_tokens *
+ * hidden + 2 * all_tokens * kv halfwords.  The staged K/V go into one of them
+ * when it is large enough (at the model's shapes both are), else into a
+ * stream-ordered allocation of the call.  Same arithmetic and output as
+ * cosmos3_qwen_gen_full_gqa_attention_f32; -1 for a null pointer or
+ * inconsistent sizes. */
+int cosmos3_qwen_gen_full_gqa_attention_workspace_f32(const float *q_gen, const float *k_all,
+                                                      const float *v_all, float *y_gen,
+                                                      float *scores_workspace, int gen_tokens,
+                                                      int all_tokens, int hidden, int kv, int q_heads,
+                                                      int kv_heads, int head_dim, hipStream_t stream);
+int cosmos3_qwen_gen_full_gqa_attention_workspace_bf16tc_f32(
+    const float *q_gen, const float *k_all, const float *v_all, float *y_gen, float *scores_workspace,
+    unsigned short *bf16_workspace, int gen_tokens, int all_tokens, int hidden, int kv, int q_heads,
+    int kv_heads, int head_dim, hipStream_t stream);
 
 /* ============================================================
  * Paged block-masked attention (one launch for a batch of sequences)
@@ -369,10 +388,9 @@ int lingbot_runtime_kv_attn_cublas_f32(const float *q, const float *cache_k,
  * row with no visible key.  q/k/v/out: f32 [seq][n_heads][head_dim], device.
  * A key block listed twice counts once (the reference would count it twice).
  * Q, K and V round to bf16 (fp32 accumulation; V of any finite magnitude: see
- * "Value range" above).  These two own a
- * device workspace (hipMalloc when a call needs more than the last one,
- * kept until exit): the first call at a new size must not be under stream
- * capture, and calls on one device from several threads must not overlap. */
+ * "Value range" above).  The K/V staging is a stream-ordered allocation of
+ * the call (hipMallocAsync, released by hipFreeAsync on the same stream):
+ * calls on different streams do not share memory. */
 int lingbot_flex_attn_f32(const float *q, const float *k, const float *v, const int *row_ptr,
                           const int *col_idx, float *out, int seq_q, int seq_k, int n_heads,
                           int head_dim, int block_size, float scale, hipStream_t stream);

@@ -204,3 +204,83 @@ def test_cosmos3_gqa_faces(emb, orc, torch_dev, D, hq, hkv):
     assert L.cosmos3_qwen_causal_gqa_attention_f32(None, None, None, None, T, hq * D, hkv * D, hq, hkv, D, None) == -1
     assert L.cosmos3_qwen_causal_gqa_attention_f32(y.data_ptr(), y.data_ptr(), y.data_ptr(), y.data_ptr(), T,
                                                    hq * D + 1, hkv * D, hq, hkv, D, None) == -1
+
+
+@pytest.mark.parametrize("G,T,hq,hkv,D", [(51, 300, 8, 2, 128), (1, 64, 4, 1, 64)])
+def test_cosmos3_gen_full_workspace_faces(emb, orc, torch_dev, G, T, hq, hkv, D):
+    """cosmos3_qwen_gen_full_gqa_attention_workspace_f32 and _workspace_bf16tc_f32
+    (kernels/cosmos3/cosmos3_qwen_language_cuda.h:105-134), the symbols the MoT
+    denoise calls (models/cosmos3.cpp:7889, :8187), with caller workspaces of
+    the model's sizes: bit-identical to the workspace-free face (same
+    arithmetic), within the bar of the oracle rounded to bf16, and the
+    workspaces' contents are scratch.  The second shape's workspaces are too
+    small for the staging (one generated token): the call allocates instead."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(G * 3 + D)
+    bf = lambda shape: orc.f32_to_bf16(rng.standard_normal(shape).astype(np.float32))
+    q, k, v = bf((G, hq, D)), bf((T, hkv, D)), bf((T, hkv, D))
+    f = lambda a: torch.from_numpy(orc.bf16_to_f32(a).reshape(a.shape[0], -1).copy()).to(dev)
+    qd, kd, vd = f(q), f(k), f(v)
+    L = emb.lib()
+    args = (G, T, hq * D, hkv * D, hq, hkv, D)
+    y0 = torch.full((G, hq * D), float("nan"), dtype=torch.float32, device=dev)
+    assert L.cosmos3_qwen_gen_full_gqa_attention_f32(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), y0.data_ptr(),
+                                                     *args, None) == 0, emb.last_error()
+    scores = torch.full((G * T * (hq // hkv),), 7.0, dtype=torch.float32, device=dev)
+    bfw = torch.zeros(G * hq * D + 2 * T * hkv * D, dtype=torch.int16, device=dev)
+    y1 = torch.full_like(y0, float("nan"))
+    assert L.cosmos3_qwen_gen_full_gqa_attention_workspace_f32(
+        qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), y1.data_ptr(), scores.data_ptr(), *args, None) == 0, \
+        emb.last_error()
+    y2 = torch.full_like(y0, float("nan"))
+    assert L.cosmos3_qwen_gen_full_gqa_attention_workspace_bf16tc_f32(
+        qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), y2.data_ptr(), scores.data_ptr(), bfw.data_ptr(), *args,
+        None) == 0, emb.last_error()
+    torch.cuda.synchronize()
+    a0, a1, a2 = (t.cpu().numpy() for t in (y0, y1, y2))
+    assert np.array_equal(a0, a1) and np.array_equal(a0, a2)
+    rb = lambda a: orc.bf16_to_f32(orc.f32_to_bf16(a))
+    ref = rb(orc.gqa_attention(q, k, v, G, T, hq, hkv, D, 1 / math.sqrt(D)))
+    assert_close(a1.reshape(G, hq, D), ref, "gen full workspace")
+    # the reference's argument checks (:1152-1158, :1190-1196)
+    assert L.cosmos3_qwen_gen_full_gqa_attention_workspace_f32(
+        qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), y1.data_ptr(), None, *args, None) == -1
+    assert L.cosmos3_qwen_gen_full_gqa_attention_workspace_bf16tc_f32(
+        qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), y2.data_ptr(), scores.data_ptr(), None, *args, None) == -1
+    bad = (G, T, hq * D + 1, hkv * D, hq, hkv, D)
+    assert L.cosmos3_qwen_gen_full_gqa_attention_workspace_f32(
+        qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), y1.data_ptr(), scores.data_ptr(), *bad, None) == -1
+
+
+def test_faces_on_two_streams(emb, orc, torch_dev):
+    """Two flex calls of different sizes in flight on two streams at once: each
+    call stages into its own stream-ordered allocation, so neither result is
+    disturbed by the other (both bit-identical to the same calls run alone)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(5)
+    cases = []
+    for sq, sk in ((64, 400), (40, 90)):
+        H, D, bs = 2, 64, 16
+        q = _bf16_valued(orc, rng, (sq, H, D))
+        k = _bf16_valued(orc, rng, (sk, H, D))
+        v = _bf16_valued(orc, rng, (sk, H, D))
+        rp, ci = _random_csr(rng, (sq + bs - 1) // bs, (sk + bs - 1) // bs, 0.8)
+        cases.append([_dev(torch, dev, x) for x in (q, k, v, rp, ci)] + [sq, sk, H, D, bs])
+    def run(c, out, stream):
+        q, k, v, rp, ci, sq, sk, H, D, bs = c
+        emb.flex_attention(q, k, v, rp, ci, out, sq, sk, H, D, bs, 0.125, stream=stream)
+    alone = []
+    for c in cases:
+        o = torch.zeros((c[5], c[7], c[8]), dtype=torch.float32, device=dev)
+        run(c, o, None)
+        torch.cuda.synchronize()
+        alone.append(o.cpu().numpy())
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [torch.zeros((c[5], c[7], c[8]), dtype=torch.float32, device=dev) for c in cases]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        run(cases[0], outs[0], s1)
+        run(cases[1], outs[1], s2)
+    torch.cuda.synchronize()
+    for a, o in zip(alone, outs):
+        assert np.array_equal(a, o.cpu().numpy())
