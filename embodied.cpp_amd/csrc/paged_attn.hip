@@ -59,9 +59,16 @@
 
 #include <climits>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "emb_common.h"
+
+// Split-K scratch of emb_paged_attention_noalloc: the partials of a call live
+// here instead of in a caller workspace.  One copy per device the library
+// runs on, held until the process ends; every call on a device shares it.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)48 << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -1476,9 +1483,49 @@ int runtime_kv_attn(const float *q, const float *cache_k, const float *cache_v, 
     return run_attention(&a, seq_q, seq_k, stream);
 }
 
+// Device address of `scratch` on the current device, looked up on the first
+// call there (hipGetSymbolAddress with that device current) and kept.
+std::mutex g_scratch_mu;
+constexpr int MAX_DEVICES = 64;
+void *g_scratch_ptr[MAX_DEVICES] = {};
+
+int scratch_on_current_device(void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "hipGetDevice failed");
+    if (dev < 0 || dev >= MAX_DEVICES) return emb::set_error(EMB_ERR_UNSUPPORTED, "device ordinal %d", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return emb::set_error(EMB_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return EMB_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int emb_paged_attention_noalloc(const emb_attn_args *a, hipStream_t stream) {
+    EMB_CHECK_ARG(a, "null args");
+    EMB_CHECK_ARG(!a->workspace, "workspace must be NULL: the split-K partials go to the library's scratch");
+    if (a->splits <= 1) return run_attention(a, 0, 0, stream);
+    const size_t need = emb_attn_workspace_bytes(a->batch, a->max_q, a->hq, a->hkv, a->head_dim, a->splits);
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return emb::set_error(EMB_ERR_CAPACITY,
+                              "split-K partials of this call need %zu bytes; the no-allocation scratch holds %zu "
+                              "(fewer splits, or emb_paged_attention with a workspace)",
+                              need, NOALLOC_SCRATCH_BYTES);
+    void *ptr = nullptr;
+    const int rc = scratch_on_current_device(&ptr);
+    if (rc) return rc;
+    emb_attn_args b = *a;
+    b.workspace = ptr;
+    return run_attention(&b, 0, 0, stream);
+}
 
 size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_t hkv, int32_t head_dim,
                                 int32_t splits) {

@@ -108,6 +108,7 @@ _SIGS = {
                                 C.c_int32, vp]),
     "emb_attn_workspace_bytes": (C.c_size_t, [C.c_int32] * 6),
     "emb_paged_attention": (C.c_int, [C.POINTER(AttnArgs), vp]),
+    "emb_paged_attention_noalloc": (C.c_int, [C.POINTER(AttnArgs), vp]),
     "lingbot_runtime_kv_update_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int,
                                                 C.c_int, vp]),
     "lingbot_runtime_kv_gather_f32": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int,
@@ -454,7 +455,7 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
                     valid_stride=0, mask_kind=EMB_MASK_FULL, chunk=0, window=-1, mask=None,
                     mask_q_stride=0, mask_batch_stride=0, block_map=None, block_size=0,
                     block_map_cols=0, block_map_batch_stride=0, splits=1, workspace=None,
-                    n_keys_uniform=0, out_bf16_round=False, stream=None):
+                    n_keys_uniform=0, out_bf16_round=False, stream=None, noalloc=False):
     a = AttnArgs()
     a.q = ptr(q); a.q_is_f32 = int(q_is_f32)
     a.q_stride = q_stride if q_stride is not None else hq * d
@@ -471,6 +472,8 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
     a.block_map_batch_stride = block_map_batch_stride
     a.splits = splits; a.workspace = ptr(workspace); a.n_keys_uniform = n_keys_uniform
     a.out_bf16_round = int(out_bf16_round)
+    if noalloc:  # split-K partials in the library's scratch (workspace must be None)
+        return check(lib().emb_paged_attention_noalloc(C.byref(a), stream_ptr(stream)), "emb_paged_attention_noalloc")
     return check(lib().emb_paged_attention(C.byref(a), stream_ptr(stream)), "emb_paged_attention")
 
 

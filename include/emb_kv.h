@@ -341,6 +341,19 @@ typedef struct emb_attn_args {
 size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_t hkv,
                                 int32_t head_dim, int32_t splits);
 int emb_paged_attention(const emb_attn_args *a, hipStream_t stream);
+/* No counterpart in the reference: emb_paged_attention for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, except that workspace
+ * must be NULL: the split-K partials go to a scratch array the library holds
+ * on each device (48 MiB, for as long as the process runs; at most
+ * emb_attn_workspace_bytes() of it per call: config 1's 18-layer launch at 3
+ * splits takes 14.6 MB, config 3's layer at 4 splits 43.3 MB).  A call whose
+ * partials need more returns EMB_ERR_CAPACITY before any launch.  Calls no
+ * hipMalloc / hipFree; the first call on a device looks the scratch address
+ * up.  Every call on one device shares the scratch (nothing in it must start
+ * zeroed; each split writes its rows before the merge reads them), so calls
+ * that overlap on one device -- several streams, or several threads -- race. */
+int emb_paged_attention_noalloc(const emb_attn_args *a, hipStream_t stream);
 
 /* ============================================================
  * Reference-named kernel-level face (same signatures as
