@@ -290,6 +290,13 @@ __global__ __launch_bounds__(NT) void meta_update_kernel(DevCache c, int32_t key
             }
         }
     }
+    if (!ok) {
+        // downstream launches on this stream (append, attention) must see no
+        // keys rather than the previous call's lists: every slot -1 (skipped
+        // by the append), no valid slot
+        for (int32_t i = t; i < key_size; i += NT) slots[i] = -1;
+        if (t == 0 && n_valid) n_valid[0] = 0;
+    }
     if (t == 0) status[0] = ok ? EMB_OK : EMB_ERR_CAPACITY;
 }
 
@@ -364,7 +371,14 @@ int emb_dev_cache_update(const emb_dev_slot_cache *c, int32_t key_size, int32_t 
     else
         hipLaunchKernelGGL(meta_update_kernel<false>, dim3(1), dim3(NT), 0, stream, dev(c), key_size, mode, slots,
                            valid, n_valid, status);
-    return launched("emb_dev_cache_update");
+    if (int rc = launched("emb_dev_cache_update")) return rc;
+    // Evicting every visible slot frees the whole cache, so the call fails
+    // exactly when key_size > capacity: known here, without waiting for the
+    // device.  (The kernel still ran: the evictions persist, as in
+    // allocate_slots_into, and it wrote slots -1 and n_valid 0.)
+    if (key_size > c->capacity)
+        return emb::set_error(EMB_ERR_CAPACITY, "key_size %d exceeds the cache capacity %d", key_size, c->capacity);
+    return EMB_OK;
 }
 
 int emb_dev_cache_restore(const emb_dev_slot_cache *c, const int32_t *slots, int32_t n, hipStream_t stream) {

@@ -18,6 +18,7 @@ LIB_PATH = PKG / "libemb_kv.so"
 _lib = None
 
 EMB_MASK_FULL, EMB_MASK_CHUNK, EMB_MASK_TOKEN, EMB_MASK_ADD, EMB_MASK_BLOCKMAP = range(5)
+EMB_ERR_ARG, EMB_ERR_LAUNCH, EMB_ERR_CAPACITY, EMB_ERR_UNSUPPORTED = -1, -2, -3, -4
 
 i32p = C.POINTER(C.c_int32)
 i64p = C.POINTER(C.c_int64)
@@ -232,10 +233,18 @@ class DevSlotCache:
         check(lib().emb_dev_cache_init(C.byref(self.desc), stream_ptr(stream)), "emb_dev_cache_init")
 
     def update(self, key_size, mode, stream=None, with_valid=True):
-        check(lib().emb_dev_cache_update(C.byref(self.desc), key_size, mode, ptr(self.slots),
-                                         ptr(self.valid) if with_valid else None,
-                                         ptr(self.n_valid) if with_valid else None, ptr(self.status),
-                                         stream_ptr(stream)), "emb_dev_cache_update")
+        """The returned status is the device's; last_rc the call's own return
+        code (EMB_ERR_CAPACITY, not raised, when key_size > capacity)."""
+        if key_size > self.slots.numel():  # slots[key_size] is written even on failure (all -1)
+            import torch
+            self.slots = torch.empty(key_size, dtype=torch.int32, device=self.slots.device)
+        rc = lib().emb_dev_cache_update(C.byref(self.desc), key_size, mode, ptr(self.slots),
+                                        ptr(self.valid) if with_valid else None,
+                                        ptr(self.n_valid) if with_valid else None, ptr(self.status),
+                                        stream_ptr(stream))
+        self.last_rc = rc
+        if rc != EMB_ERR_CAPACITY:
+            check(rc, "emb_dev_cache_update")
         return self.slots[:key_size], self.valid, self.n_valid, self.status
 
     def restore(self, slots, n, stream=None):

@@ -181,8 +181,11 @@ int emb_dev_cache_init(const emb_dev_slot_cache *c, hipStream_t stream);
  * collect_valid_slots (:8967-8972); mode 0: prepare_mode0_temp_slots_no_insert
  * (:8904-8944).  Device outputs: slots[key_size] (ascending), valid[capacity]
  * (may be NULL) and *n_valid (may be NULL), *status = 0, or EMB_ERR_CAPACITY
- * when even evicting every visible slot leaves fewer than key_size free (the
- * evictions stay, as in allocate_slots_into, :8793-8831). */
+ * when even evicting every visible slot leaves fewer than key_size free, i.e.
+ * key_size > capacity: the evictions stay, as in allocate_slots_into
+ * (:8793-8831), slots[] is set to -1 and *n_valid to 0 (so an append and an
+ * attention queued after it see no keys), and the call itself also returns
+ * EMB_ERR_CAPACITY. */
 int emb_dev_cache_update(const emb_dev_slot_cache *c, int32_t key_size, int32_t mode, int32_t *slots,
                          int32_t *valid, int32_t *n_valid, int32_t *status, hipStream_t stream);
 int emb_dev_cache_restore(const emb_dev_slot_cache *c, const int32_t *slots, int32_t n,

@@ -205,15 +205,26 @@ def test_null_block_tables_are_identity(emb, orc, torch_dev, d, hq, hkv, mask):
         assert_close(outs[(1, "null")][b * nq:(b + 1) * nq], ref, f"null tables seq {b}")
 
 
-def test_multi_session_sweep(emb, orc, torch_dev):
-    """cfg4: sessions with prefix lengths U[300,1200] + 51 queries, pages scattered in one pool."""
+@pytest.mark.parametrize("B,splits", [(1, 8), (8, 8), (32, 2), (64, 1), (64, 2)])
+def test_multi_session_sweep(emb, orc, torch_dev, B, splits):
+    """cfg4 at every batch the bench times, with its prefix lengths and split
+    choices: session b's prefix is 300 + x_b % 901, x_b the b-th output of
+    std::mt19937_64(0xE3BD0004); 51 queries x 8 heads over prefix + 51 keys,
+    pages scattered in one pool.  All rows of every session at B <= 8; 24
+    sampled rows of every session at B = 32 and 64."""
     torch, dev = torch_dev
-    rng = np.random.default_rng(0xE3BD0004)
-    L = rng.integers(300, 1201, 8)
-    s = Seqs(orc, rng, [int(x) + 51 for x in L], [51] * 8, 8, 1, 256)
-    got = s.run(emb, torch, dev, 1 / 16)
-    for b in range(8):
-        assert_close(got[b], s.oracle(orc, b, 1 / 16), f"session {b}")
+    lens = [300 + orc.lib().orc_mt64_nth(0xE3BD0004, b + 1) % 901 for b in range(B)]
+    assert 300 <= min(lens) and max(lens) <= 1200
+    rng = np.random.default_rng(0xE3BD0004 + B)
+    s = Seqs(orc, rng, [int(x) + 51 for x in lens], [51] * B, 8, 1, 256)
+    got = s.run(emb, torch, dev, 1 / 16, splits=splits)
+    for b in range(B):
+        rows = None if B <= 8 else np.sort(rng.choice(51, 3, replace=False))
+        ref = s.oracle(orc, b, 1 / 16, rows=rows)
+        if rows is None:
+            assert_close(got[b], ref, f"B={B} session {b}")
+        else:
+            assert_close(got[b][rows], ref[rows], f"B={B} session {b} rows {rows.tolist()}")
 
 
 def test_prefill_prefix_lm_rows(emb, orc, torch_dev):

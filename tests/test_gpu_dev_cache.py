@@ -64,8 +64,12 @@ def _replay(emb, orc, torch, dev, cap, ops, legacy):
             sb = o.update_meta(k, pred)
             torch.cuda.synchronize()
             if sb is None:
-                assert int(st.item()) == CAPACITY_ERR, what
+                # failure (k > capacity): status and return code say so, and what
+                # a queued append / attention would read lists no key
+                assert int(st.item()) == CAPACITY_ERR and d.last_rc == CAPACITY_ERR, what
+                assert np.all(slots.cpu().numpy() == -1) and int(nv.item()) == 0, what
             else:
+                assert d.last_rc == 0, what
                 assert int(st.item()) == 0, what
                 assert np.array_equal(slots.cpu().numpy(), sb), what
                 vb = o.collect_valid()
@@ -79,7 +83,8 @@ def _replay(emb, orc, torch, dev, cap, ops, legacy):
             sb, vb = o.prepare_mode0(k)
             torch.cuda.synchronize()
             if sb is None:
-                assert int(st.item()) == CAPACITY_ERR, what
+                assert int(st.item()) == CAPACITY_ERR and d.last_rc == CAPACITY_ERR, what
+                assert np.all(slots.cpu().numpy() == -1) and int(nv.item()) == 0, what
             else:
                 assert int(st.item()) == 0, what
                 assert np.array_equal(slots.cpu().numpy(), sb), what

@@ -247,3 +247,74 @@ def test_w8_tile_heights_agree(emb, orc, torch_dev):
     rows = np.array([0, 127, 128, 255, 256, 299, 512, 1535, 1536, 1559], np.int64)
     _, yf_ref = orc.w8a16_gemm(x, q, s_st, M, K, N, rows=rows)
     assert_close(wide[rows], yf_ref, "w8 wide rows")
+
+
+def test_config5_fused_qkv_then_config3_attention(emb, orc, torch_dev):
+    """BASELINE configs[4] end to end at full size: x 1560 x 3072 bf16 through
+    the W8 projection to 9216 (int8 weights, per-channel bf16 scales), Q to a
+    buffer and K/V appended straight into the config-3 paged cache (24 heads,
+    D 128, capacity 14040 = 9 chunks, the 8 earlier chunks already there,
+    pages permuted), then the config-3 attention of the new chunk over all
+    14040 keys (split-K 4, the bench's).  Each link against the oracle: the
+    fused Q and pool (K, V, f16 shadow) bit-exact to the oracle's paged append
+    of the plain GEMM's bf16 output; that GEMM within the W8 bar of the oracle
+    on sampled rows; the attention within the north-star bar of the oracle
+    over the same K/V on sampled query tokens (all 24 heads each)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0005)
+    M, K, H, D = 1560, 3072, 24, 128
+    n_q = H * D
+    N = 3 * n_q
+    cap = 9 * M
+    prior = 8 * M
+    n_pages = (cap + 15) // 16
+    w, q, s, s_st = _weights(orc, rng, K, N)
+    x = orc.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    bt = rng.permutation(n_pages + 7)[:n_pages].astype(np.int32)
+    page_elems = H * 16 * D
+    kp0 = np.zeros((n_pages + 7) * page_elems, np.uint16)
+    vp0 = np.zeros_like(kp0)
+    kprior = orc.f32_to_bf16(rng.standard_normal((prior, H, D)).astype(np.float32))
+    vprior = orc.f32_to_bf16(rng.standard_normal((prior, H, D)).astype(np.float32))
+    orc.paged_append(kprior, vprior, n_q, np.arange(prior, dtype=np.int32), bt, H, D, cap, kp0, vp0)
+    slots = (prior + np.arange(M)).astype(np.int32)
+    x_d, q_d, s_d = _t(torch, dev, x), _t(torch, dev, q), _t(torch, dev, s_st)
+    kp, vp = _t(torch, dev, kp0), _t(torch, dev, vp0)
+    v16 = _t(torch, dev, v16_shadow(vp0, D))
+    bt_d = _t(torch, dev, bt)
+    qo = torch.zeros((M, n_q), dtype=torch.int16, device=dev)
+    emb.w8a16_qkv_append(x_d, q_d, s_d, M, K, n_q, qo, _t(torch, dev, slots), bt_d, cap, kp, vp, H, D, v16_pool=v16)
+    out = torch.full((M, H, D), float("nan"), dtype=torch.float32, device=dev)
+    splits = 4
+    ws = torch.empty(emb.attn_workspace_bytes(1, M, H, H, D, splits) // 4 + 4, dtype=torch.float32, device=dev)
+    emb.paged_attention(q=qo, out=out, k_pool=kp, v_pool=vp, v16_pool=v16, batch=1, hq=H, hkv=H, d=D, max_q=M,
+                        scale=1 / np.sqrt(D), capacity=cap, cu_q=_t(torch, dev, np.array([0, M], np.int32)),
+                        n_keys=_t(torch, dev, np.array([cap], np.int32)), block_tables=bt_d, bt_stride=n_pages,
+                        splits=splits, workspace=ws)
+    torch.cuda.synchronize()
+    # link 1: the fused projection + append against the oracle append of the plain GEMM
+    yb = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_BF16)
+    qb = qo.cpu().numpy().view(np.uint16)
+    assert np.array_equal(qb, yb[:, :n_q])
+    kexp, vexp = kp0.copy(), vp0.copy()
+    knew = np.ascontiguousarray(yb[:, n_q:2 * n_q])
+    vnew = np.ascontiguousarray(yb[:, 2 * n_q:])
+    orc.paged_append(knew, vnew, n_q, slots, bt, H, D, cap, kexp, vexp)
+    assert np.array_equal(kp.cpu().numpy().view(np.uint16), kexp), "K pages differ"
+    assert np.array_equal(vp.cpu().numpy().view(np.uint16), vexp), "V pages differ"
+    assert np.array_equal(v16.cpu().numpy().view(np.uint16), v16_shadow(vexp, D)), "V shadow differs"
+    # link 2: that GEMM against the oracle (fp32 value on sampled rows, bf16 bar)
+    rows = np.array([0, 255, 256, 777, 1023, 1024, 1559], np.int64)
+    yb_ref, _ = orc.w8a16_gemm(x, q, s_st, M, K, N, rows=rows)
+    _check_bf16(yb[rows], yb_ref[rows] if yb_ref.shape[0] == M else yb_ref, "config-5 gemm rows", orc)
+    # link 3: the attention over exactly these keys against the oracle
+    kall = np.concatenate([kprior, knew.reshape(M, H, D)])
+    vall = np.concatenate([vprior, vnew.reshape(M, H, D)])
+    toks = np.array([0, 389, 390, 1000, 1559], np.int64)
+    ref = orc.gqa_attention(qb.reshape(M, H, D), kall, vall, M, cap, H, H, D, 1 / np.sqrt(D), rows=toks)
+    # The new keys and values are W8 outputs, not N(0,1): y has a standard
+    # deviation of s * sqrt(K) * sigma_w (about 4 to 40 here), so the bar is
+    # applied to the output divided by V's RMS, as for any V scale.
+    v_rms = float(np.sqrt(np.mean(orc.bf16_to_f32(vall).astype(np.float64) ** 2)))
+    assert v_rms > 1.5
+    assert_close(out.cpu().numpy()[toks] / v_rms, ref[toks] / v_rms, "config-3 attention after the fused projection")
