@@ -154,9 +154,9 @@ class PagedLayers:
                              self.new_slots, self.bt, self.L * self.cap, self.k_pool, self.v_pool,
                              self.hkv, self.d, stream=stream, v16_pool=self.v16_pool)
 
-    def attend(self, step, stream, scale):
+    def attend(self, step, stream, scale, q=None):
         s = step % self.n_steps
-        self.c.emb.paged_attention(q=self.q[s], out=self.out, k_pool=self.k_pool, v_pool=self.v_pool,
+        self.c.emb.paged_attention(q=self.q[s] if q is None else q, out=self.out, k_pool=self.k_pool, v_pool=self.v_pool,
                                    v16_pool=self.v16_pool,
                                    batch=self.L, hq=self.hq, hkv=self.hkv, d=self.d, max_q=self.n_new,
                                    scale=scale, capacity=self.cap,
@@ -247,6 +247,30 @@ def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
             lp.attend(0, st, scale)
     ms_layer, _ = c.time_graph(per_layer, max(2, steps // 2), 2)
 
+    # the pi0.5 producer in place of the plain append: the expert's f32 Q/K/V
+    # projection outputs go through NEOX RoPE at positions 816 + i
+    # (models/pi05.cpp:394-402) into a bf16 Q and the cache, then attention
+    # reads that Q -- one producer launch for the 18 layers' 51 tokens
+    torch, emb = c.torch, c.emb
+    T = n_layers * n_new
+    q32 = c.synth(0xE3BD0300, T * hq * d).view(torch.bfloat16).float()
+    k32 = c.synth(0xE3BD0301, T * hkv * d).view(torch.bfloat16).float()
+    v32 = c.synth(0xE3BD0302, T * hkv * d).view(torch.bfloat16).float()
+    q_roped = torch.zeros(T * hq * d, dtype=torch.int16, device=c.dev)
+    positions = c.i32(np.tile(n_pref + np.arange(n_new), n_layers))
+
+    def produce(st):
+        emb.qkv_neox_rope_append(q32, hq * d, k32, hkv * d, v32, hkv * d, T, hq, hkv, d, q_roped, P.new_slots,
+                                 P.bt, P.L * P.cap, P.k_pool, P.v_pool, v16_pool=P.v16_pool, positions=positions,
+                                 q_out_f32=False, stream=st)
+    ms_prod, _ = c.time_graph(produce, steps, warmup)
+
+    def produce_attend(st):
+        produce(st)
+        P.attend(0, st, scale, q=q_roped)
+    ms_prod_step, _ = c.time_graph(produce_attend, steps, warmup)
+    prod_bytes = T * (hq + 2 * hkv) * d * 4 + T * hq * d * 2 + 3 * T * hkv * d * 2 + T * 4 * 2
+
     # cold vs warm: eager steps, each after 1 GiB is rewritten on the stream
     # (flushes the 256 MB MALL and the L2s; outside the timed region) or not
     cold_us, warm_us = cold_warm_steps(c, one_step, n=max(5, steps // 4))
@@ -259,6 +283,10 @@ def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
         us_per_step_warm_eager=warm_us,
         us_per_step_10step_graph=ms_ten * 1e3 / 10,
         us_per_step_dependent_layers=ms_layer * 1e3,
+        us_per_step_with_neox_producer=ms_prod_step * 1e3,
+        neox_producer_us=ms_prod * 1e3,
+        neox_producer_bytes=prod_bytes,
+        neox_producer_gbs=prod_bytes / (ms_prod * 1e-3) / 1e9,
         attn_us_single_launch=attn_us,
         attn_us_avg_in_graph=attn_avg_us,
         splits=best[0],

@@ -102,6 +102,9 @@ _SIGS = {
     "emb_qkv_rownorm_rope_append": (C.c_int, [vp, C.c_int64, C.c_int32, C.c_int32, C.c_int32, vp, vp, vp,
                                               C.c_float, vp, vp, vp, C.c_int64, vp, vp, C.c_int32, vp, vp,
                                               vp, vp]),
+    "emb_qkv_neox_rope_append": (C.c_int, [vp, C.c_int64, vp, C.c_int64, vp, C.c_int64, C.c_int32, C.c_int32,
+                                           C.c_int32, C.c_int32, vp, C.c_int32, C.c_float, vp, C.c_int32,
+                                           C.c_int64, vp, vp, C.c_int32, vp, vp, vp, vp]),
     "emb_qkv_norm_rope_append": (C.c_int, [vp, C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp,
                                            C.c_float, C.c_int32, C.c_float, C.c_int32, vp, vp, C.c_int64, vp,
                                            vp, C.c_int32, vp, vp, vp, vp]),
@@ -392,6 +395,25 @@ def qkv_rownorm_rope_append(qkv, ld, tokens, heads, d, q_out, slots, block_table
                                                     ptr(block_table), capacity, ptr(k_pool), ptr(v_pool),
                                                     ptr(v16_pool), stream_ptr(stream)),
                  "emb_qkv_rownorm_rope_append")
+
+
+def qkv_neox_rope_append(q, ld_q, k, ld_k, v, ld_v, tokens, q_heads, kv_heads, d, q_out, slots, block_table,
+                         capacity, k_pool, v_pool, v16_pool=None, positions=None, first_position=0,
+                         freq_base=10000.0, q_out_f32=True, ldq=None, stream=None):
+    """pi0.5 NEOX RoPE (ggml_rope_ext, mode NEOX, n_dims = d) on f32 Q and K plus
+    the paged K/V append (emb_qkv_neox_rope_append)."""
+    _need_rows(q, tokens, ld_q, q_heads * d, 4, "q")
+    _need_rows(k, tokens, ld_k, kv_heads * d, 4, "k")
+    _need_rows(v, tokens, ld_v, kv_heads * d, 4, "v")
+    _need_rows(q_out, tokens, ldq or q_heads * d, q_heads * d, 4 if q_out_f32 else 2, "q_out")
+    _need_bytes(positions, tokens * 4, "positions")
+    _need_bytes(slots, tokens * 4, "slots")
+    return check(lib().emb_qkv_neox_rope_append(ptr(q), ld_q, ptr(k), ld_k, ptr(v), ld_v, tokens, q_heads,
+                                                 kv_heads, d, ptr(positions), first_position, freq_base,
+                                                 ptr(q_out), int(bool(q_out_f32)), ldq or q_heads * d,
+                                                 ptr(slots), ptr(block_table), capacity, ptr(k_pool),
+                                                 ptr(v_pool), ptr(v16_pool), stream_ptr(stream)),
+                 "emb_qkv_neox_rope_append")
 
 
 def kv_gather(k_pool, v_pool, valid, n, block_table, capacity, k_out, v_out, hkv, d, stream=None):

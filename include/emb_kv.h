@@ -239,6 +239,30 @@ int emb_qkv_rownorm_rope_append(const float *qkv, int64_t ld, int32_t tokens, in
                                 const int32_t *slots, const int32_t *block_table, int32_t capacity,
                                 void *k_pool, void *v_pool, void *v16_pool, hipStream_t stream);
 
+/* pi0.5 form: NEOX RoPE on the f32 Q and K projections and the K/V append, in
+ * one launch -- replaces build_adarms_gemma_layer's (and build_gemma_layer's)
+ * ggml_rope_ext(t, positions, NULL, head_dim, GGML_ROPE_TYPE_NEOX, 0,
+ * freq_base, 1, 0, 1, 32, 1) on q and k and the ggml_concat of k_rope / v onto
+ * the cached prefix (models/pi05.cpp:394-408, :308-325; suffix positions
+ * n_prefix + i at :876-878, prefix positions i at :872-874).
+ * q: f32 [tokens][ld_q] (q_heads heads of head_dim), k and v: f32
+ * [tokens][ld_k] / [tokens][ld_v] (kv_heads heads) -- three mul_mat outputs,
+ * or column ranges of one fused row.  Position of token i: positions[i]
+ * (device int32 [tokens]) or, with positions NULL, first_position + i.
+ * For pair i < head_dim/2 of a head, theta = pos * theta_scale^i with
+ * theta_scale = freq_base^(-2/head_dim) (f32, ggml's rule), and
+ * (x[i], x[i + head_dim/2]) -> (x0 cos - x1 sin, x0 sin + x1 cos) in f32.
+ * Q goes to q_out [tokens][ldq], f32 (q_out_f32 nonzero) or bf16; K and V go
+ * into the cache in bf16 at slots[token] (skip rules and layout of
+ * emb_kv_append; f16 V shadow when v16_pool).  head_dim % 8 == 0; q, k, v 16-byte
+ * aligned, ld_q / ld_k / ld_v / ldq multiples of 4. */
+int emb_qkv_neox_rope_append(const float *q, int64_t ld_q, const float *k, int64_t ld_k, const float *v,
+                             int64_t ld_v, int32_t tokens, int32_t q_heads, int32_t kv_heads,
+                             int32_t head_dim, const int32_t *positions, int32_t first_position,
+                             float freq_base, void *q_out, int32_t q_out_f32, int64_t ldq,
+                             const int32_t *slots, const int32_t *block_table, int32_t capacity,
+                             void *k_pool, void *v_pool, void *v16_pool, hipStream_t stream);
+
 /* Reference-named Cosmos3 language-tower attention faces
  * (kernels/cosmos3/cosmos3_qwen_language_cuda.h:77-112, called from
  * models/cosmos3.cpp:5032,7889,8187): f32 q [tokens][hidden], k/v

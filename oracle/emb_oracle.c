@@ -847,3 +847,33 @@ void orc_head_norm_rope(const uint16_t *x, int64_t ld, int64_t tokens, int64_t h
     }
     free(v);
 }
+
+/* ---------------- pi0.5 NEOX RoPE (ggml_rope_ext, GGML_ROPE_TYPE_NEOX) ----------------
+ * Call sites: models/pi05.cpp:308-314 (prefix layers) and :394-400 (expert
+ * layers), n_dims = head_dim, freq_scale 1, ext_factor 0, attn_factor 1,
+ * positions from :872-878.  ggml itself (llama.cpp b9016) is not vendored; this
+ * restates its published f32 rope for its CUDA backend: theta_scale =
+ * powf(freq_base, -2 / n_dims); pair i of a row at position pos turns by
+ * theta = pos * powf(theta_scale, i) (freq_scale 1 and ext_factor 0 leave
+ * theta as is; attn_factor 1 scales cos/sin by 1), and (x[i], x[i + n/2])
+ * -> (x0 cos - x1 sin, x0 sin + x1 cos).  f32 throughout, each product rounded
+ * on its own (the build uses -ffp-contract=off); libm powf/cosf/sinf. */
+void orc_neox_rope_f32(const float *x, int64_t ld, int64_t tokens, int64_t heads, int64_t d,
+                       const int32_t *pos, int64_t first_pos, float freq_base, float *out, int64_t out_ld) {
+    const int64_t half = d / 2;
+    const float theta_scale = powf(freq_base, -2.0f / (float)d);
+    for (int64_t t = 0; t < tokens; ++t) {
+        const float p = (float)(pos ? (int64_t)pos[t] : first_pos + t);
+        for (int64_t h = 0; h < heads; ++h) {
+            const float *xr = x + t * ld + h * d;
+            float *o = out + t * out_ld + h * d;
+            for (int64_t i = 0; i < half; ++i) {
+                const float theta = p * powf(theta_scale, (float)i);
+                const float c = cosf(theta), s = sinf(theta);
+                const float x0 = xr[i], x1 = xr[i + half];
+                o[i] = x0 * c - x1 * s;
+                o[i + half] = x0 * s + x1 * c;
+            }
+        }
+    }
+}

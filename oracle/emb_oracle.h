@@ -159,6 +159,11 @@ void    orc_w8a16_gemm(const uint16_t *x, const int32_t *qweight, const uint16_t
 void orc_head_norm_rope(const uint16_t *x, int64_t ld, int64_t tokens, int64_t heads, int64_t d,
                         const uint16_t *gamma, float eps, int rope_kind, float theta, int64_t first_pos,
                         const int32_t *pos_ids, uint16_t *out, int64_t out_ld);
+/* pi0.5 NEOX RoPE in f32 (ggml_rope_ext at models/pi05.cpp:308-314,394-400):
+ * x f32 [tokens][ld] (heads * d columns) -> out f32 [tokens][out_ld];
+ * position of token t: pos[t], or first_pos + t when pos is NULL. */
+void orc_neox_rope_f32(const float *x, int64_t ld, int64_t tokens, int64_t heads, int64_t d,
+                       const int32_t *pos, int64_t first_pos, float freq_base, float *out, int64_t out_ld);
 
 #ifdef __cplusplus
 }

@@ -68,6 +68,8 @@ _SIGS = {
                                    C.c_int64, C.c_float, C.c_int]),
     "orc_head_norm_rope": (None, [u16p, C.c_int64, C.c_int64, C.c_int64, C.c_int64, u16p, C.c_float, C.c_int,
                                   C.c_float, C.c_int64, i32p, u16p, C.c_int64]),
+    "orc_neox_rope_f32": (None, [f32p, C.c_int64, C.c_int64, C.c_int64, C.c_int64, i32p, C.c_int64, C.c_float,
+                                 f32p, C.c_int64]),
     "orc_gqa_attention_bf16": (None, [u16p, u16p, u16p, C.c_int64, C.c_int64, C.c_int64,
                                       C.c_int64, C.c_int64, C.c_float, u8p, f32p, C.c_int64,
                                       C.c_int64, C.c_int64, i64p, C.c_int64, C.c_int, f32p]),
@@ -413,4 +415,16 @@ def head_norm_rope(x, tokens, heads, d, gamma=None, eps=1e-6, rope_kind=0, theta
     pid = None if pos_ids is None else np.ascontiguousarray(pos_ids, np.int32)
     lib().orc_head_norm_rope(P(x, u16p), ld, tokens, heads, d, P(g, u16p), C.c_float(eps), rope_kind,
                              C.c_float(theta), first_pos, P(pid, i32p), P(out, u16p), heads * d)
+    return out.reshape(tokens, heads, d)
+
+
+def neox_rope(x, tokens, heads, d, positions=None, first_pos=0, freq_base=10000.0, ld=None):
+    """pi0.5 NEOX RoPE (orc_neox_rope_f32): f32 x [tokens][ld] (heads*d columns
+    used) -> f32 [tokens][heads][d]."""
+    x = np.ascontiguousarray(x, np.float32)
+    ld = ld or heads * d
+    out = np.zeros(tokens * heads * d, np.float32)
+    pos = None if positions is None else np.ascontiguousarray(positions, np.int32)
+    lib().orc_neox_rope_f32(P(x, f32p), ld, tokens, heads, d, P(pos, i32p), first_pos, C.c_float(freq_base),
+                            P(out, f32p), heads * d)
     return out.reshape(tokens, heads, d)

@@ -525,3 +525,93 @@ def test_lingbot_qkv_bias_then_norm(orc):
     w = np.ones(H * D, np.float32)
     q2, _, _ = orc.lingbot_qkv(x, H, D, bias=b, q_w=w)
     assert np.array_equal(q2, orc.lingbot_row_norm(xb[:, :H * D], w))
+
+
+# ---------------- pi0.5 NEOX RoPE (ggml_rope_ext, models/pi05.cpp:394-400) ----------------
+def _neox64(x, pos, d, base=10000.0):
+    """float64 rotation of the f32 input: pair (i, i + d/2) by pos * base^(-2i/d)."""
+    x = x.astype(np.float64)
+    half = d // 2
+    th = np.asarray(pos, np.float64)[:, None] * base ** (-2.0 * np.arange(half) / d)[None, :]
+    c, s = np.cos(th)[:, None, :], np.sin(th)[:, None, :]
+    x0, x1 = x[..., :half], x[..., half:]
+    return np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], axis=-1), th
+
+
+def test_neox_rope_identity_onehots_and_known_answer(orc):
+    rng = np.random.default_rng(41)
+    T, H, D = 5, 3, 256
+    x = rng.standard_normal((T, H * D)).astype(np.float32)
+    # position 0 turns nothing: cos 0 = 1 and sin 0 = 0 leave every value exact
+    assert np.array_equal(orc.neox_rope(x, T, H, D, first_pos=0)[0], x.reshape(T, H, D)[0])
+    # NEOX pairs dim i with i + D/2 (not 2i with 2i + 1): a one-hot at i lands on
+    # i (cos) and i + D/2 (sin) only; a one-hot at i + D/2 on i (-sin) and i + D/2 (cos)
+    pos = 5
+    for i in (0, 1, 7, D // 2 - 1):
+        th = pos * 10000.0 ** (-2.0 * i / D)
+        for src, (a, b) in ((i, (math.cos(th), math.sin(th))), (i + D // 2, (-math.sin(th), math.cos(th)))):
+            e = np.zeros((1, D), np.float32)
+            e[0, src] = 1.0
+            y = orc.neox_rope(e, 1, 1, D, first_pos=pos)[0, 0].astype(np.float64)
+            nz = set(np.flatnonzero(y).tolist())
+            assert nz <= {i, i + D // 2}, (i, src, sorted(nz))
+            assert abs(y[i] - a) < 1e-5 and abs(y[i + D // 2] - b) < 1e-5, (i, src, y[i], y[i + D // 2])
+    # pair 0 turns by exactly pos radians (theta_scale^0 = 1): position 1 is a turn by 1 rad
+    e = np.zeros((1, D), np.float32)
+    e[0, 0] = 1.0
+    y = orc.neox_rope(e, 1, 1, D, first_pos=1)[0, 0]
+    assert y[0] == np.float32(math.cos(1.0)) and y[D // 2] == np.float32(math.sin(1.0))
+
+
+def test_neox_rope_float64_and_pair_lengths(orc):
+    # against float64 at the config-1 suffix positions (n_prefix 816 + i): the
+    # only gap is f32 theta, whose relative error grows with the power i of the
+    # rounded theta_scale (about (i + 4) ulp), plus the f32 sin/cos/products
+    rng = np.random.default_rng(42)
+    T, H, D = 51, 9, 256
+    x = (rng.standard_normal((T, H * D)) * 3).astype(np.float32)
+    pos = 816 + np.arange(T)
+    y = orc.neox_rope(x, T, H, D, first_pos=816).astype(np.float64)
+    want, th = _neox64(x.reshape(T, H, D), pos, D)
+    half = D // 2
+    n_in = np.hypot(x.reshape(T, H, D)[..., :half].astype(np.float64), x.reshape(T, H, D)[..., half:])
+    dth = th * (np.arange(half) + 4) * 2.0 ** -24 + 4 * 2.0 ** -24  # angle error bound [T][half]
+    tol = np.concatenate([n_in * dth[:, None, :]] * 2, axis=-1) + 1e-6
+    err = np.abs(y - want)
+    assert np.all(err <= tol), float(np.max(err / tol))
+    # a rotation: each (i, i + D/2) pair keeps its length
+    n_out = np.hypot(y[..., :half], y[..., half:])
+    assert np.allclose(n_out, n_in, rtol=2e-6, atol=1e-6)
+    # the explicit positions array reads the same as first_pos + t
+    assert np.array_equal(orc.neox_rope(x, T, H, D, positions=pos.astype(np.int32)), y.astype(np.float32))
+
+
+def test_neox_rope_relative_position_and_cpu_rule(orc):
+    # RoPE's defining property: <rope(q, m), rope(k, n)> depends on m - n only
+    rng = np.random.default_rng(43)
+    D = 256
+    q = rng.standard_normal((1, D)).astype(np.float32)
+    k = rng.standard_normal((1, D)).astype(np.float32)
+    dots = []
+    for m, n in ((820, 816), (4, 0), (104, 100)):
+        a = orc.neox_rope(q, 1, 1, D, first_pos=m)[0, 0].astype(np.float64)
+        b = orc.neox_rope(k, 1, 1, D, first_pos=n)[0, 0].astype(np.float64)
+        dots.append(a @ b)
+    assert max(dots) - min(dots) < 1e-5 * np.linalg.norm(q) * np.linalg.norm(k), dots
+    # ggml's CPU backend builds theta by repeated multiplication (theta *=
+    # theta_scale per pair) instead of one power per pair; the two f32 rules
+    # agree within the f32 theta error bound above
+    T, H = 51, 1
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    ts = np.float32(np.float32(10000.0) ** np.float32(-2.0 / D))
+    th = np.zeros((T, D // 2), np.float32)
+    for t in range(T):
+        v = np.float32(816 + t)
+        for i in range(D // 2):
+            th[t, i] = v
+            v = np.float32(v * ts)
+    c, s = np.cos(th.astype(np.float64)), np.sin(th.astype(np.float64))
+    x0, x1 = x[:, :D // 2].astype(np.float64), x[:, D // 2:].astype(np.float64)
+    cpu = np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], axis=-1)
+    y = orc.neox_rope(x, T, H, D, first_pos=816)[:, 0].astype(np.float64)
+    assert np.max(np.abs(y - cpu)) < 5e-3 * np.max(np.abs(x)), np.max(np.abs(y - cpu))
