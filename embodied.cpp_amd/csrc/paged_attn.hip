@@ -139,9 +139,11 @@ struct KParams {
     int32_t valid_stride;
     int32_t capacity;
     int32_t batch, hq, hkv, G;
+    int32_t max_q;
     int32_t row_tiles;
     int32_t splits;
     int32_t total_wg;
+    float scale;
     float c_log2;     // scale * log2(e)
     float th_raw;     // RESCALE_TH / c_log2
     float inv_scale;  // 1 / scale (additive masks are added in raw score units)
@@ -1308,6 +1310,206 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
 }
 
 
+// ---- Attention with bf16 probabilities (SmolVLA's rounding) ----
+//
+// Reference: build_self_attn_layer and build_cross_attn_layer
+// (models/smolvla.cpp:255-266, :309-318): kq = mul_mat(K, Q) in f32, attn =
+// bf16_round(soft_max_ext(kq, mask, 1/sqrt(hd))), kqv = mul_mat(V, attn) -- the
+// probabilities are normalised, then rounded to bf16, then multiplied with V.
+// Normalised probabilities need the row's max and sum before any P.V term, so
+// this path makes two passes over the keys, a wave per (query token, head) row:
+//   pass 1: a lane per key computes s = (q . k) * scale (+ additive mask, or
+//           -inf where hidden), keeping a per-lane running max and sum of
+//           exp; one wave reduction gives the row's m and l;
+//   pass 2: per 64 keys, a lane per key recomputes s and stores
+//           p = bf16(exp(s - m) * (1/l)) in LDS; then the lanes, over dims,
+//           accumulate p * v in f32 -- on the paged path 16 keys of a page per
+//           32-byte V load.
+// The query row is rounded to bf16 (as on the MFMA path) and broadcast from
+// LDS.  K/V addressing, zero rows and masks are the main kernel's.  Not tuned:
+// it serves the small SmolVLA shapes, where it is latency-bound.
+template <int D, int MASK, bool VALID, bool QF32>
+__global__ __launch_bounds__(256) void attn_pbf16_kernel(KParams p) {
+    constexpr int E = D / 64;  // dims a lane accumulates
+    __shared__ __attribute__((aligned(16))) float qs[4][D];
+    __shared__ float ps[4][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * 4 + wave;
+    const int64_t per_b = (int64_t)p.max_q * p.hq;
+    const int32_t b = (int32_t)min(r / per_b, (int64_t)p.batch - 1);
+    const int32_t qi = (int32_t)((r % per_b) / p.hq), h = (int32_t)(r % p.hq);
+    const int32_t q_begin = p.cu_q ? p.cu_q[b] : b * p.nq_single;
+    const int32_t nq = p.cu_q ? p.cu_q[b + 1] - q_begin : p.nq_single;
+    const int32_t nk = p.n_keys ? p.n_keys[b] : p.nk_single;
+    const bool live = r < (int64_t)p.batch * per_b && qi < nq;  // wave-uniform
+    const int32_t tok = qi;
+    const int32_t qpos = (p.q_pos0 ? p.q_pos0[b] : nk - nq) + tok;
+    const int32_t kvh = h / p.G;
+    const int32_t *valid_b = VALID ? p.valid + (int64_t)b * p.valid_stride : nullptr;
+    const int32_t *bt_b = p.bt ? p.bt + (int64_t)b * p.bt_stride : nullptr;
+    const int32_t lim = VALID ? p.capacity : min(p.capacity, p.bt ? p.bt_stride * 16 : p.capacity);
+
+    for (int d = lane; d < D; d += 64) {
+        float x = 0.0f;
+        if (live) {
+            const int64_t off = (int64_t)(q_begin + tok) * p.q_stride + (int64_t)h * D + d;
+            x = QF32 ? bf16_to_f32(f32_to_bf16_bits(reinterpret_cast<const float *>(p.q)[off]))
+                     : bf16_to_f32(reinterpret_cast<const uint16_t *>(p.q)[off]);
+        }
+        qs[wave][d] = x;
+    }
+    __syncthreads();
+
+    // page of key j's slot, or -1 for a zero row
+    auto key_page = [&](int32_t j, int32_t &t) -> int32_t {
+        const int32_t sl = VALID ? valid_b[j] : j;
+        t = sl & 15;
+        if (sl < 0 || sl >= lim) return -1;
+        return page_of(bt_b, sl);
+    };
+    // masked, scaled score of key j (-inf when hidden)
+    auto score = [&](int32_t j) -> float {
+        int32_t t;
+        const int32_t pg = key_page(j, t);
+        float dot = 0.0f;
+        if (pg >= 0) {
+            const uint16_t *kr = p.k_pool + (((int64_t)pg * p.hkv + kvh) * 16 + t) * D;
+#pragma unroll 4
+            for (int c = 0; c < D / 8; ++c) {
+                const u32x4 w = *reinterpret_cast<const u32x4 *>(kr + c * 8);
+                const f32x4 qa = *reinterpret_cast<const f32x4 *>(&qs[wave][c * 8]);
+                const f32x4 qb = *reinterpret_cast<const f32x4 *>(&qs[wave][c * 8 + 4]);
+                dot += qa[0] * bf16_to_f32(w[0] & 0xffffu) + qa[1] * bf16_to_f32(w[0] >> 16) +
+                       qa[2] * bf16_to_f32(w[1] & 0xffffu) + qa[3] * bf16_to_f32(w[1] >> 16) +
+                       qb[0] * bf16_to_f32(w[2] & 0xffffu) + qb[1] * bf16_to_f32(w[2] >> 16) +
+                       qb[2] * bf16_to_f32(w[3] & 0xffffu) + qb[3] * bf16_to_f32(w[3] >> 16);
+            }
+        }
+        float x = dot * p.scale;
+        bool vis = true;
+        if (MASK == EMB_MASK_CHUNK) {
+            const int32_t qc = qpos / p.chunk, kc = j / p.chunk;
+            vis = kc <= qc && (p.window < 0 || qc - kc <= p.window);
+        } else if (MASK == EMB_MASK_TOKEN) {
+            vis = reinterpret_cast<const uint8_t *>(p.mask)[(int64_t)b * p.mask_b_stride + (int64_t)tok * p.mask_q_stride +
+                                                            j] != 0;
+        } else if (MASK == EMB_MASK_ADD) {
+            x += reinterpret_cast<const float *>(p.mask)[(int64_t)b * p.mask_b_stride + (int64_t)tok * p.mask_q_stride +
+                                                         j];
+        }
+        return vis ? x : -INFINITY;
+    };
+
+    // pass 1: row max and sum of exp
+    float m = -INFINITY, l = 0.0f;
+    if (live) {
+        for (int32_t j = lane; j < nk; j += 64) {
+            const float x = score(j);
+            if (x > m) {
+                l = l * expf(m - x) + 1.0f;
+                m = x;
+            } else if (x > -INFINITY) {
+                l += expf(x - m);
+            }
+        }
+    }
+    float mr = m;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mr = fmaxf(mr, __shfl_xor(mr, off, 64));
+    float lr = mr > -INFINITY && m > -INFINITY ? l * expf(m - mr) : 0.0f;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) lr += __shfl_xor(lr, off, 64);
+    const bool any = mr > -INFINITY;  // a row with no visible key stores zeros
+    const float inv_l = any ? 1.0f / lr : 0.0f;
+
+    // pass 2: P.V with P = bf16(exp(s - m) / l)
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = 0.0f;
+    const int32_t kend = live && any ? nk : 0;
+    for (int32_t j0 = 0; j0 < kend; j0 += 64) {
+        const int32_t j = j0 + lane;
+        float pj = 0.0f;
+        if (j < nk) {
+            const float x = score(j);
+            pj = x > -INFINITY ? bf16_to_f32(f32_to_bf16_bits(expf(x - mr) * inv_l)) : 0.0f;
+        }
+        ps[wave][lane] = pj;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int n = min(64, nk - j0);
+        if (!VALID) {
+            // keys j0 .. j0+n-1 are slots j0.. : 16 keys of a page per V load
+            for (int pg0 = 0; pg0 < n; pg0 += 16) {
+                const int32_t sl = j0 + pg0;
+                int32_t page = sl < lim ? page_of(bt_b, sl) : -1;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int d = lane + 64 * e;
+                    u32x4 w0 = {0u, 0u, 0u, 0u}, w1 = w0;
+                    if (page >= 0) {
+                        const uint16_t *vr = p.v_pool + (((int64_t)page * p.hkv + kvh) * D + d) * 16;
+                        w0 = *reinterpret_cast<const u32x4 *>(vr);
+                        w1 = *reinterpret_cast<const u32x4 *>(vr + 8);
+                    }
+#pragma unroll
+                    for (int t = 0; t < 16; ++t) {
+                        if (pg0 + t >= n || sl + t >= lim) break;
+                        const uint32_t wd = t < 8 ? w0[t >> 1] : w1[(t - 8) >> 1];
+                        acc[e] += ps[wave][pg0 + t] * bf16_to_f32((t & 1) ? wd >> 16 : wd & 0xffffu);
+                    }
+                }
+            }
+        } else {
+            for (int jj = 0; jj < n; ++jj) {
+                int32_t t;
+                const int32_t pg = key_page(j0 + jj, t);
+                if (pg < 0) continue;
+                const float pv = ps[wave][jj];
+#pragma unroll
+                for (int e = 0; e < E; ++e)
+                    acc[e] += pv * bf16_to_f32(p.v_pool[(((int64_t)pg * p.hkv + kvh) * D + lane + 64 * e) * 16 + t]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (!live) return;
+    float *dst = p.out + (int64_t)(q_begin + tok) * p.out_stride + (int64_t)h * D;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const float o = acc[e];
+        dst[lane + 64 * e] = p.round_out ? bf16_to_f32(f32_to_bf16_bits(o)) : o;
+    }
+}
+
+template <int D, int MASK>
+hipError_t launch_pbf16(const KParams &kp, bool valid, bool qf32, hipStream_t stream) {
+    const int64_t rows = (int64_t)kp.batch * kp.max_q * kp.hq;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (valid && qf32)
+        hipLaunchKernelGGL((attn_pbf16_kernel<D, MASK, true, true>), grid, dim3(256), 0, stream, kp);
+    else if (valid)
+        hipLaunchKernelGGL((attn_pbf16_kernel<D, MASK, true, false>), grid, dim3(256), 0, stream, kp);
+    else if (qf32)
+        hipLaunchKernelGGL((attn_pbf16_kernel<D, MASK, false, true>), grid, dim3(256), 0, stream, kp);
+    else
+        hipLaunchKernelGGL((attn_pbf16_kernel<D, MASK, false, false>), grid, dim3(256), 0, stream, kp);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t dispatch_pbf16(const KParams &kp, int mask, bool valid, bool qf32, hipStream_t stream) {
+    switch (mask) {
+        case EMB_MASK_FULL: return launch_pbf16<D, EMB_MASK_FULL>(kp, valid, qf32, stream);
+        case EMB_MASK_CHUNK: return launch_pbf16<D, EMB_MASK_CHUNK>(kp, valid, qf32, stream);
+        case EMB_MASK_TOKEN: return launch_pbf16<D, EMB_MASK_TOKEN>(kp, valid, qf32, stream);
+        default: return launch_pbf16<D, EMB_MASK_ADD>(kp, valid, qf32, stream);
+    }
+}
+
 template <int D, int MASK, int LD, bool QF32>
 hipError_t launch_kernel(const KParams &kp, hipStream_t stream) {
     const int grid = (kp.total_wg + 7) / 8 * 8;
@@ -1421,6 +1623,8 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     const int64_t total = (int64_t)a->batch * a->hkv * splits * kp.row_tiles;
     EMB_CHECK_ARG(total < INT_MAX / 2, "grid too large");
     kp.total_wg = (int32_t)total;
+    kp.scale = a->scale;
+    kp.max_q = a->max_q;
     kp.c_log2 = a->scale * LOG2E;
     kp.th_raw = RESCALE_TH / kp.c_log2;
     kp.inv_scale = 1.0f / a->scale;
@@ -1438,9 +1642,22 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
         kp.ws_o = (uint16_t *)a->workspace;
         kp.ws_ml = reinterpret_cast<float *>(kp.ws_o + rows_all * a->head_dim);
     }
-    const int ld = a->valid_slots ? LD_VALID : (a->v16_pool ? LD_DMA : LD_REG);
     const bool qf32 = a->q_is_f32 != 0;
     hipError_t e;
+    if (a->p_bf16) {
+        EMB_CHECK_ARG(splits == 1, "p_bf16 runs unsplit (splits must be 0 or 1)");
+        EMB_CHECK_ARG(a->mask_kind != EMB_MASK_BLOCKMAP, "p_bf16 takes no block map");
+        EMB_CHECK_ARG((int64_t)a->batch * a->max_q * a->hq / 4 < INT_MAX, "grid too large");
+        const bool valid = a->valid_slots != nullptr;
+        switch (a->head_dim) {
+            case 64: e = dispatch_pbf16<64>(kp, a->mask_kind, valid, qf32, stream); break;
+            case 128: e = dispatch_pbf16<128>(kp, a->mask_kind, valid, qf32, stream); break;
+            default: e = dispatch_pbf16<256>(kp, a->mask_kind, valid, qf32, stream); break;
+        }
+        if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "p_bf16 attention launch: %s", hipGetErrorString(e));
+        return EMB_OK;
+    }
+    const int ld = a->valid_slots ? LD_VALID : (a->v16_pool ? LD_DMA : LD_REG);
     switch (a->head_dim) {
         case 64: e = dispatch_mask<64>(kp, a->mask_kind, ld, qf32, stream); break;
         case 128: e = dispatch_mask<128>(kp, a->mask_kind, ld, qf32, stream); break;

@@ -44,6 +44,7 @@ class AttnArgs(C.Structure):
         ("splits", C.c_int32), ("workspace", vp),
         ("n_keys_uniform", C.c_int32),
         ("out_bf16_round", C.c_int32),
+        ("p_bf16", C.c_int32),
     ]
 
 
@@ -102,6 +103,13 @@ _SIGS = {
     "emb_qkv_rownorm_rope_append": (C.c_int, [vp, C.c_int64, C.c_int32, C.c_int32, C.c_int32, vp, vp, vp,
                                               C.c_float, vp, vp, vp, C.c_int64, vp, vp, C.c_int32, vp, vp,
                                               vp, vp]),
+    "emb_hy_patch_groups": (C.c_int32, [vp, C.c_int32, vp]),
+    "emb_hy_prefix_mask": (C.c_int, [C.c_int64, vp, vp, vp]),
+    "emb_hy_suffix_mask": (C.c_int, [C.c_int64, C.c_int64, vp, vp]),
+    "emb_groot_layer_mask_kind": (C.c_int, [C.c_int32, C.c_int32]),
+    "emb_groot_cross_masks": (C.c_int, [vp, vp, C.c_int64, C.c_int64, vp, vp]),
+    "emb_smolvla_masks": (C.c_int, [vp, C.c_int64, C.c_int64, vp, vp, vp]),
+    "emb_smolvla_positions": (C.c_int, [vp, C.c_int64, C.c_int64, vp, vp, vp]),
     "emb_qkv_neox_rope_append": (C.c_int, [vp, C.c_int64, vp, C.c_int64, vp, C.c_int64, C.c_int32, C.c_int32,
                                            C.c_int32, C.c_int32, vp, C.c_int32, C.c_float, vp, C.c_int32,
                                            C.c_int64, vp, vp, C.c_int32, vp, vp, vp, vp]),
@@ -358,6 +366,62 @@ def synth_normal_bf16(seed: int, n: int) -> np.ndarray:
     return out
 
 
+# ---- call-site masks (host; numpy in, numpy out) ----
+def hy_patch_groups(modality_mask):
+    m = np.ascontiguousarray(modality_mask, np.int32)
+    g = np.full(max(len(m), 1), -1, np.int32)
+    n = check(lib().emb_hy_patch_groups(ptr(m), len(m), ptr(g)), "emb_hy_patch_groups")
+    return n, g[:len(m)]
+
+
+def hy_prefix_mask(n, group_of=None):
+    """(u8 allow [n][n], f16 bits [n][n]) of HY-VLA's prefix mask."""
+    allow = np.zeros((n, n), np.uint8)
+    f16 = np.zeros((n, n), np.uint16)
+    g = None if group_of is None else np.ascontiguousarray(group_of, np.int32)
+    check(lib().emb_hy_prefix_mask(n, ptr(g), ptr(allow), ptr(f16)), "emb_hy_prefix_mask")
+    return allow, f16
+
+
+def hy_suffix_mask(n_pref, n_suf):
+    allow = np.zeros((n_suf, n_pref + n_suf), np.uint8)
+    f16 = np.zeros((n_suf, n_pref + n_suf), np.uint16)
+    check(lib().emb_hy_suffix_mask(n_pref, n_suf, ptr(allow), ptr(f16)), "emb_hy_suffix_mask")
+    return allow, f16
+
+
+def groot_layer_mask_kind(layer, attend_text_every_n_blocks=2):
+    return check(lib().emb_groot_layer_mask_kind(layer, attend_text_every_n_blocks), "emb_groot_layer_mask_kind")
+
+
+def groot_cross_masks(attention_mask, image_flags, n_q):
+    a = np.ascontiguousarray(attention_mask, np.int32)
+    im = np.ascontiguousarray(image_flags, np.int32)
+    text = np.zeros((n_q, len(a)), np.float32)
+    image = np.zeros((n_q, len(a)), np.float32)
+    check(lib().emb_groot_cross_masks(ptr(a), ptr(im), len(a), n_q, ptr(text), ptr(image)), "emb_groot_cross_masks")
+    return text, image
+
+
+def smolvla_masks(prefix_valid, n_suf):
+    v = np.ascontiguousarray(prefix_valid, np.uint8)
+    n = len(v)
+    pm = np.zeros((n, n), np.float32)
+    fm = np.zeros((n_suf, n + n_suf), np.float32)
+    cm = np.zeros((n_suf, n), np.float32)
+    check(lib().emb_smolvla_masks(ptr(v), n, n_suf, ptr(pm), ptr(fm), ptr(cm)), "emb_smolvla_masks")
+    return pm, fm, cm
+
+
+def smolvla_positions(prefix_valid, n_suf):
+    v = np.ascontiguousarray(prefix_valid, np.uint8)
+    pp = np.zeros(len(v), np.int32)
+    sp = np.zeros(max(n_suf, 1), np.int32)
+    cp = np.zeros(max(n_suf, 1), np.int32)
+    check(lib().emb_smolvla_positions(ptr(v), len(v), n_suf, ptr(pp), ptr(sp), ptr(cp)), "emb_smolvla_positions")
+    return pp, sp[:n_suf], cp[:n_suf]
+
+
 def kv_append(k_new, v_new, src_stride, n, slots, block_table, capacity, k_pool, v_pool, hkv, d,
               stream=None, v16_pool=None):
     return check(lib().emb_kv_append(ptr(k_new), ptr(v_new), src_stride, n, ptr(slots),
@@ -486,7 +550,7 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
                     valid_stride=0, mask_kind=EMB_MASK_FULL, chunk=0, window=-1, mask=None,
                     mask_q_stride=0, mask_batch_stride=0, block_map=None, block_size=0,
                     block_map_cols=0, block_map_batch_stride=0, splits=1, workspace=None,
-                    n_keys_uniform=0, out_bf16_round=False, stream=None, noalloc=False):
+                    n_keys_uniform=0, out_bf16_round=False, stream=None, noalloc=False, p_bf16=False):
     a = AttnArgs()
     a.q = ptr(q); a.q_is_f32 = int(q_is_f32)
     a.q_stride = q_stride if q_stride is not None else hq * d
@@ -503,6 +567,7 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
     a.block_map_batch_stride = block_map_batch_stride
     a.splits = splits; a.workspace = ptr(workspace); a.n_keys_uniform = n_keys_uniform
     a.out_bf16_round = int(out_bf16_round)
+    a.p_bf16 = int(p_bf16)
     if noalloc:  # split-K partials in the library's scratch (workspace must be None)
         return check(lib().emb_paged_attention_noalloc(C.byref(a), stream_ptr(stream)), "emb_paged_attention_noalloc")
     return check(lib().emb_paged_attention(C.byref(a), stream_ptr(stream)), "emb_paged_attention")

@@ -134,6 +134,48 @@ int64_t emb_cross_block_table(const emb_flex_meta *m, int32_t *row_ptr, int32_t 
 int emb_self_token_mask(const emb_flex_meta *m, uint8_t *mask);                /* :9456-9465 */
 
 /* ============================================================
+ * Call-site masks and positions (host): what the reference's model graphs
+ * build before ggml's attention ops, as u8 "visible" masks for
+ * EMB_MASK_TOKEN / f32 additive masks for EMB_MASK_ADD, and in the
+ * reference's own additive form (0 / -inf) for emb_ggml_flash_attn_ext.
+ * Row = query, column = key.
+ * ============================================================ */
+/* HY-VLA make_visual_patch_groups (models/hy_vla.cpp:1251-1277): runs of
+ * nonzero modality flags, a single zero not ending a group; group_of[i] = the
+ * group of token i or -1.  Returns the group count. */
+int32_t emb_hy_patch_groups(const int32_t *modality_mask, int32_t n, int32_t *group_of);
+/* HY-VLA make_prefix_mask (models/hy_vla.cpp:1279-1306) [n][n]: causal, but
+ * among patch-group tokens a key is visible iff it is in the query's group
+ * (bidirectional inside a group, cross-group pairs hidden); group_of NULL =
+ * plain causal (:2131).  allow: u8 1 = visible; mask_f16: the reference's F16
+ * bits (0x0000 / 0xFC00).  Either may be NULL. */
+int emb_hy_prefix_mask(int64_t n, const int32_t *group_of, uint8_t *allow, uint16_t *mask_f16);
+/* HY-VLA expert-with-prefix mask (models/hy_vla.cpp:2831-2843)
+ * [n_suf][n_pref + n_suf]: all prefix keys; suffix row 0 (state) sees only
+ * itself among the suffix, other rows the whole suffix. */
+int emb_hy_suffix_mask(int64_t n_pref, int64_t n_suf, uint8_t *allow, uint16_t *mask_f16);
+/* GR00T DiT (models/groot_n1.cpp:656-661): 0 = self-attention layer (no
+ * mask), 1 = cross-attention with the text mask, 2 = with the image mask. */
+int emb_groot_layer_mask_kind(int32_t layer, int32_t attend_text_every_n_blocks);
+/* GR00T cross-attention masks (models/groot_n1.cpp:708-716), f32 additive
+ * [n_q][n_keys]: text = valid and not image, image = valid and image.  Either
+ * output may be NULL. */
+int emb_groot_cross_masks(const int32_t *attention_mask, const int32_t *image_flags, int64_t n_keys, int64_t n_q,
+                          float *text_mask, float *image_mask);
+/* SmolVLA masks (models/smolvla.cpp:696-725), f32 additive; any may be NULL:
+ * prefix [n_prefix][n_prefix] (invalid keys hidden; the last prefix token,
+ * the state, hidden from the other queries), full [n_suf][n_prefix + n_suf]
+ * (invalid prefix keys hidden, causal inside the suffix), cross
+ * [n_suf][n_prefix] (invalid prefix keys hidden). */
+int emb_smolvla_masks(const uint8_t *prefix_valid, int64_t n_prefix, int64_t n_suf, float *prefix_mask,
+                      float *full_mask, float *cross_mask);
+/* SmolVLA RoPE positions (models/smolvla.cpp:680-688): prefix i at
+ * max(valid tokens in [0, i] - 1, 0), suffix i at (valid prefix tokens) + i,
+ * cross-attention queries at i.  Any output may be NULL. */
+int emb_smolvla_positions(const uint8_t *prefix_valid, int64_t n_prefix, int64_t n_suf, int32_t *prefix_pos,
+                          int32_t *suffix_pos, int32_t *cross_pos);
+
+/* ============================================================
  * Device data movement (bf16 pool)
  * ============================================================ */
 
@@ -363,6 +405,12 @@ typedef struct emb_attn_args {
     int32_t out_bf16_round;            /* nonzero: every output value is stored rounded to
                                           bf16 precision (nearest even), still as f32 -- the
                                           Cosmos3 kernels' output rounding, done in the store */
+    int32_t p_bf16;                    /* nonzero: the softmax probabilities are normalised and
+                                          rounded to bf16 before P.V, f32 accumulation
+                                          (SmolVLA's bf16_round(soft_max_ext(...)),
+                                          models/smolvla.cpp:264-266, :317-318); a two-pass
+                                          kernel, unsplit (splits 0 or 1), masks FULL, CHUNK,
+                                          TOKEN or ADD; the f16 V shadow is not read */
 } emb_attn_args;
 
 size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_t hkv,

@@ -428,3 +428,145 @@ def neox_rope(x, tokens, heads, d, positions=None, first_pos=0, freq_base=10000.
     lib().orc_neox_rope_f32(P(x, f32p), ld, tokens, heads, d, P(pos, i32p), first_pos, C.c_float(freq_base),
                             P(out, f32p), heads * d)
     return out.reshape(tokens, heads, d)
+
+
+# ---------------- call-site masks (restated step by step, pure Python) ----------------
+NEG_INF = float("-inf")
+
+
+def hy_patch_groups(modality_mask):
+    """make_visual_patch_groups (models/hy_vla.cpp:1251-1277): list of groups
+    (lists of token indices), following the reference's scan."""
+    groups, cur, i, n = [], [], 0, len(modality_mask)
+    while i < n:
+        if modality_mask[i] == 0:
+            z0 = i
+            while i < n and modality_mask[i] == 0:
+                i += 1
+            if i - z0 >= 2 and cur:
+                groups.append(cur)
+                cur = []
+            continue
+        while i < n and modality_mask[i] != 0:
+            cur.append(i)
+            i += 1
+    if cur:
+        groups.append(cur)
+    return groups
+
+
+def hy_prefix_mask(n, groups=None):
+    """make_prefix_mask (models/hy_vla.cpp:1279-1306): f32 additive [n][n] built
+    in the reference's three passes (causal; every patch pair -inf; each
+    group's pairs 0)."""
+    m = np.array([[0.0 if c <= r else NEG_INF for c in range(n)] for r in range(n)], np.float32)
+    if groups is not None:
+        every = [t for g in groups for t in g]
+        for r in every:
+            for c in every:
+                m[r, c] = NEG_INF
+        for g in groups:
+            for r in g:
+                for c in g:
+                    m[r, c] = 0.0
+    return m
+
+
+def hy_suffix_mask(n_pref, n_suf):
+    """full_mask of the routed predict path (models/hy_vla.cpp:2831-2843)."""
+    n_total = n_pref + n_suf
+    m = np.zeros((n_suf, n_total), np.float32)
+    for r in range(n_suf):
+        for c in range(n_total):
+            allowed = c < n_pref
+            if not allowed:
+                s = c - n_pref
+                allowed = (s == 0) if r == 0 else True
+            m[r, c] = 0.0 if allowed else NEG_INF
+    return m
+
+
+def groot_layer_mask_kind(layer, attend_text_every_n_blocks=2):
+    """models/groot_n1.cpp:656-661: 0 self-attention, 1 text mask, 2 image mask."""
+    if layer % 2 == 1:
+        return 0
+    return 1 if layer % (2 * attend_text_every_n_blocks) == 0 else 2
+
+
+def groot_cross_masks(attention_mask, image_flags, n_q):
+    """models/groot_n1.cpp:708-716: (text, image) f32 additive [n_q][n_keys]."""
+    nk = len(attention_mask)
+    text = np.zeros((n_q, nk), np.float32)
+    image = np.zeros((n_q, nk), np.float32)
+    for q in range(n_q):
+        for k in range(nk):
+            valid = attention_mask[k] != 0
+            is_image = image_flags[k] != 0
+            text[q, k] = 0.0 if valid and not is_image else NEG_INF
+            image[q, k] = 0.0 if valid and is_image else NEG_INF
+    return text, image
+
+
+def smolvla_masks(prefix_valid, n_suf):
+    """models/smolvla.cpp:696-725: (prefix [n][n], full [n_suf][n+n_suf],
+    cross [n_suf][n]) f32 additive."""
+    n = len(prefix_valid)
+    pm = np.zeros((n, n), np.float32)
+    for q in range(n):
+        for k in range(n):
+            if not prefix_valid[k] or (q < n - 1 and k == n - 1):
+                pm[q, k] = NEG_INF
+    fm = np.zeros((n_suf, n + n_suf), np.float32)
+    cm = np.zeros((n_suf, n), np.float32)
+    for q in range(n_suf):
+        for k in range(n):
+            if not prefix_valid[k]:
+                fm[q, k] = NEG_INF
+                cm[q, k] = NEG_INF
+        for k in range(q + 1, n_suf):
+            fm[q, n + k] = NEG_INF
+    return pm, fm, cm
+
+
+def smolvla_positions(prefix_valid, n_suf):
+    """models/smolvla.cpp:680-688: (prefix, suffix, cross) int32 positions."""
+    pp, pos = [], -1
+    for v in prefix_valid:
+        if v:
+            pos += 1
+        pp.append(max(pos, 0))
+    off = pos + 1
+    return (np.array(pp, np.int32), np.array([off + i for i in range(n_suf)], np.int32),
+            np.arange(n_suf, dtype=np.int32))
+
+
+def pbf16_attention(q, k, v, n_q, n_k, hq, hkv, d, scale, add=None, round_p=True):
+    """SmolVLA's attention numerics (models/smolvla.cpp:255-266): scores
+    kq = K.Q as f32 (computed in float64, rounded to f32), x = kq * scale +
+    mask (f32), softmax with the row max (f32 exp), p = e * (1/sum) rounded to
+    bf16 (round_p), out = sum_j p_j v_j (float64).  q/k/v: bf16 bits
+    [n_q][hq][d] / [n_k][hkv][d]; add: f32 [n_q][n_k] or None.  A row with no
+    visible key is 0."""
+    qf = bf16_to_f32(np.asarray(q, np.uint16)).astype(np.float64).reshape(n_q, hq, d)
+    kf = bf16_to_f32(np.asarray(k, np.uint16)).astype(np.float64).reshape(n_k, hkv, d)
+    vf = bf16_to_f32(np.asarray(v, np.uint16)).astype(np.float64).reshape(n_k, hkv, d)
+    G = hq // hkv
+    out = np.zeros((n_q, hq, d))
+    for h in range(hq):
+        kk, vv = kf[:, h // G], vf[:, h // G]
+        kq = (qf[:, h] @ kk.T).astype(np.float32)
+        x = (kq * np.float32(scale)).astype(np.float32)
+        if add is not None:
+            x = (x + np.asarray(add, np.float32)).astype(np.float32)
+        m = np.max(x, axis=1, keepdims=True)
+        ok = np.isfinite(m[:, 0])
+        with np.errstate(invalid="ignore", over="ignore"):
+            e = np.exp((x - np.where(np.isfinite(m), m, 0)).astype(np.float64)).astype(np.float32)
+        e[~ok] = 0
+        ssum = e.astype(np.float64).sum(axis=1, keepdims=True).astype(np.float32)
+        inv = np.where(ssum > 0, np.float32(1) / np.where(ssum > 0, ssum, 1), 0).astype(np.float32)
+        p = (e * inv).astype(np.float32)
+        if round_p:
+            p = bf16_to_f32(f32_to_bf16(p))
+        out[:, h] = p.astype(np.float64) @ vv
+    return out

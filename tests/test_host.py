@@ -269,3 +269,59 @@ def test_reference_f32_faces_reject_like_the_reference(emb):
         assert G(b, b, b, b, b, seq, h, d, cap, None) == -1
     assert U(None, b, b, b, b, 4, 2, 64, 64, None) == -1
     assert G(b, b, None, b, b, 4, 2, 64, 64, None) == -1
+
+
+# ---------------- call-site mask builders against the oracle's step-by-step restatement ----------------
+def _f16_bits(m):
+    return np.asarray(m, np.float32).astype(np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3])
+def test_hy_masks_match_oracle(emb, orc, seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 90))
+    # modality flags with runs and isolated / double zeros
+    mod = (rng.random(n) < 0.6).astype(np.int32)
+    n_groups, group_of = emb.hy_patch_groups(mod)
+    groups = orc.hy_patch_groups(mod.tolist())
+    assert n_groups == len(groups)
+    want_of = np.full(n, -1, np.int32)
+    for g, members in enumerate(groups):
+        want_of[members] = g
+    assert np.array_equal(group_of, want_of)
+    for with_groups in (False, True):
+        allow, f16 = emb.hy_prefix_mask(n, group_of if with_groups else None)
+        ref = orc.hy_prefix_mask(n, groups if with_groups else None)
+        assert np.array_equal(f16, _f16_bits(ref)), "F16 bits"
+        assert np.array_equal(allow, (ref == 0).astype(np.uint8))
+    n_suf = int(rng.integers(1, 60))
+    allow, f16 = emb.hy_suffix_mask(n, n_suf)
+    ref = orc.hy_suffix_mask(n, n_suf)
+    assert np.array_equal(f16, _f16_bits(ref)) and np.array_equal(allow, (ref == 0).astype(np.uint8))
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_groot_and_smolvla_masks_match_oracle(emb, orc, seed):
+    rng = np.random.default_rng(10 + seed)
+    nk, nq = int(rng.integers(1, 300)), int(rng.integers(1, 20))
+    valid = (rng.random(nk) < 0.8).astype(np.int32)
+    img = (rng.random(nk) < 0.5).astype(np.int32)
+    for a, b in zip(emb.groot_cross_masks(valid, img, nq), orc.groot_cross_masks(valid, img, nq)):
+        assert np.array_equal(a, b)
+    for every in (1, 2, 3):
+        assert [emb.groot_layer_mask_kind(i, every) for i in range(16)] == \
+               [orc.groot_layer_mask_kind(i, every) for i in range(16)]
+    npre, nsuf = int(rng.integers(1, 200)), int(rng.integers(1, 60))
+    pv = (rng.random(npre) < 0.85).astype(np.uint8)
+    for a, b in zip(emb.smolvla_masks(pv, nsuf), orc.smolvla_masks(pv.tolist(), nsuf)):
+        assert np.array_equal(a, b)
+    for a, b in zip(emb.smolvla_positions(pv, nsuf), orc.smolvla_positions(pv.tolist(), nsuf)):
+        assert np.array_equal(a, b)
+
+
+def test_mask_builders_refuse_bad_arguments(emb):
+    L = emb.lib()
+    assert L.emb_hy_prefix_mask(0, None, None, None) == emb.EMB_ERR_ARG
+    assert L.emb_hy_suffix_mask(4, 0, None, None) == emb.EMB_ERR_ARG
+    assert L.emb_groot_layer_mask_kind(-1, 2) == emb.EMB_ERR_ARG
+    assert L.emb_smolvla_masks(None, 4, 2, None, None, None) == emb.EMB_ERR_ARG

@@ -615,3 +615,89 @@ def test_neox_rope_relative_position_and_cpu_rule(orc):
     cpu = np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], axis=-1)
     y = orc.neox_rope(x, T, H, D, first_pos=816)[:, 0].astype(np.float64)
     assert np.max(np.abs(y - cpu)) < 5e-3 * np.max(np.abs(x)), np.max(np.abs(y - cpu))
+
+
+# ---------------- call-site masks (hand-derived known answers) ----------------
+I = float("-inf")
+
+
+def test_hy_patch_groups_known_answers(orc):
+    # runs of nonzero flags; one zero keeps the group open, two or more close it
+    assert orc.hy_patch_groups([0, 1, 1, 0, 1, 1, 0, 0, 1, 0]) == [[1, 2, 4, 5], [8]]
+    assert orc.hy_patch_groups([1, 1, 0, 0, 1]) == [[0, 1], [4]]
+    assert orc.hy_patch_groups([1, 0, 1, 0, 1]) == [[0, 2, 4]]
+    assert orc.hy_patch_groups([0, 0, 0]) == []
+    assert orc.hy_patch_groups([0, 0, 1, 1, 1]) == [[2, 3, 4]]
+    assert orc.hy_patch_groups([]) == []
+
+
+def test_hy_prefix_and_suffix_masks_known_answers(orc):
+    # n = 5, groups {1, 2} and {4}: causal outside the groups, a group sees
+    # itself both ways, the two groups never see each other
+    want = np.array([[0, I, I, I, I],
+                     [0, 0, 0, I, I],
+                     [0, 0, 0, I, I],
+                     [0, 0, 0, 0, I],
+                     [0, I, I, 0, 0]], np.float32)
+    assert np.array_equal(orc.hy_prefix_mask(5, [[1, 2], [4]]), want)
+    assert np.array_equal(orc.hy_prefix_mask(4), np.triu(np.full((4, 4), I, np.float32), 1))
+    # suffix (n_pref 2, n_suf 3): all prefix keys; row 0 sees only suffix key 0
+    want = np.array([[0, 0, 0, I, I],
+                     [0, 0, 0, 0, 0],
+                     [0, 0, 0, 0, 0]], np.float32)
+    assert np.array_equal(orc.hy_suffix_mask(2, 3), want)
+
+
+def test_groot_and_smolvla_masks_known_answers(orc):
+    # GR00T layers with attend_text_every_n_blocks 2: 0 text, 1 self, 2 image, 3 self, 4 text
+    assert [orc.groot_layer_mask_kind(i, 2) for i in range(6)] == [1, 0, 2, 0, 1, 0]
+    assert [orc.groot_layer_mask_kind(i, 1) for i in range(4)] == [1, 0, 1, 0]
+    text, image = orc.groot_cross_masks([1, 1, 1, 0], [0, 1, 1, 1], 2)
+    assert np.array_equal(text, np.array([[0, I, I, I]] * 2, np.float32))
+    assert np.array_equal(image, np.array([[I, 0, 0, I]] * 2, np.float32))
+    # SmolVLA: prefix [img, img, pad, lang, state], suffix of 2
+    pm, fm, cm = orc.smolvla_masks([1, 1, 0, 1, 1], 2)
+    want_pm = np.array([[0, 0, I, 0, I]] * 4 + [[0, 0, I, 0, 0]], np.float32)
+    assert np.array_equal(pm, want_pm)
+    assert np.array_equal(fm, np.array([[0, 0, I, 0, 0, 0, I],
+                                        [0, 0, I, 0, 0, 0, 0]], np.float32))
+    assert np.array_equal(cm, np.array([[0, 0, I, 0, 0]] * 2, np.float32))
+    pp, sp, cp = orc.smolvla_positions([1, 1, 0, 1, 1], 2)
+    assert pp.tolist() == [0, 1, 1, 2, 3] and sp.tolist() == [4, 5] and cp.tolist() == [0, 1]
+    pp, _, _ = orc.smolvla_positions([0, 0, 1], 1)
+    assert pp.tolist() == [0, 0, 0]
+
+
+def test_pbf16_attention_known_answers(orc):
+    D = 64
+    rng = np.random.default_rng(61)
+    one = orc.f32_to_bf16(np.ones(1, np.float32))[0]
+    # three equal scores: p = bf16(1/3) = 0x3EAB (0.333984375), so a V of ones
+    # gives 3 * 0.333984375 = 1.001953125, not 1
+    q = np.zeros((1, 1, D), np.uint16)
+    k = np.zeros((3, 1, D), np.uint16)
+    v = np.full((3, 1, D), one, np.uint16)
+    out = orc.pbf16_attention(q, k, v, 1, 3, 1, 1, D, 0.125)
+    assert np.all(out == 1.001953125)
+    third = np.float64(np.float32(1) / np.float32(3))  # f32 p without the bf16 rounding
+    assert np.all(orc.pbf16_attention(q, k, v, 1, 3, 1, 1, D, 0.125, round_p=False) == 3 * third)
+    # two equal scores: p = 0.5 exactly; one visible key: p = 1 (output = v)
+    vv = orc.f32_to_bf16(rng.standard_normal((3, 1, D)).astype(np.float32))
+    vf = orc.bf16_to_f32(vv).astype(np.float64)
+    add = np.array([[0, 0, I]], np.float32)
+    assert np.array_equal(orc.pbf16_attention(q, k, vv, 1, 3, 1, 1, D, 0.125, add=add)[0, 0],
+                          (vf[0, 0] + vf[1, 0]) / 2)
+    add = np.array([[I, 0, I]], np.float32)
+    assert np.array_equal(orc.pbf16_attention(q, k, vv, 1, 3, 1, 1, D, 0.125, add=add)[0, 0], vf[1, 0])
+    # without the rounding it is the (pinned) f32 attention oracle
+    n_q, n_k, hq, hkv = 7, 40, 4, 2
+    qb = orc.f32_to_bf16(rng.standard_normal((n_q, hq, D)).astype(np.float32))
+    kb = orc.f32_to_bf16(rng.standard_normal((n_k, hkv, D)).astype(np.float32))
+    vb = orc.f32_to_bf16(rng.standard_normal((n_k, hkv, D)).astype(np.float32))
+    a = orc.pbf16_attention(qb, kb, vb, n_q, n_k, hq, hkv, D, 0.125, round_p=False)
+    b = orc.gqa_attention(qb, kb, vb, n_q, n_k, hq, hkv, D, 0.125, q_pos0=0)
+    assert np.allclose(a, b, atol=2e-6), np.max(np.abs(a - b))
+    # and the rounding moves it by about bf16's precision of p (2^-9 relative)
+    r = orc.pbf16_attention(qb, kb, vb, n_q, n_k, hq, hkv, D, 0.125)
+    rel = np.abs(r - a).sum() / np.abs(a).sum()
+    assert 1e-4 < rel < 3e-3, rel
