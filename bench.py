@@ -236,9 +236,22 @@ def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
             P.attend(s, st, scale)
     ms_ten, _ = c.time_graph(ten_steps, max(2, steps // 4), 2)
 
-    # dependent per-layer launches (model-realistic ordering): 18 x (append, attention)
+    # one layer's attention alone (what a model that runs its layers in order sees
+    # per layer): average launch time of k_launch launches in one graph, by split
     single = PagedLayers(c, 0xE3BD0000, [n_pref], n_new, hq, hkv, d, n_steps=1)
-    single.set_splits(8)
+
+    def single_many(st):
+        for _ in range(k_launch):
+            single.attend(0, st, scale)
+    sweep1 = {}
+    for sp in (1, 2, 4, 8, 16):
+        single.set_splits(sp)
+        ms1, _ = c.time_graph(single_many, max(2, steps // 4), 2)
+        sweep1[sp] = ms1 * 1e3 / k_launch
+    best1 = min(sweep1, key=sweep1.get)
+    single.set_splits(best1)
+
+    # dependent per-layer launches (model-realistic ordering): 18 x (append, attention)
     layers = [single] * n_layers  # same shapes; the graph holds 36 dependent launches
 
     def per_layer(st):
@@ -283,6 +296,9 @@ def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
         us_per_step_warm_eager=warm_us,
         us_per_step_10step_graph=ms_ten * 1e3 / 10,
         us_per_step_dependent_layers=ms_layer * 1e3,
+        attn_us_single_layer=sweep1[best1],
+        single_layer_splits=best1,
+        single_layer_split_sweep_us=sweep1,
         us_per_step_with_neox_producer=ms_prod_step * 1e3,
         neox_producer_us=ms_prod * 1e3,
         neox_producer_bytes=prod_bytes,
@@ -702,7 +718,7 @@ def cpu_baseline(target_s=10.0):
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = _box_threads()
     n_pref, n_new, hq, hkv, d = 816, 51, 8, 1, 256
     nk = n_pref + n_new
     k = oracle.bf16_to_f32(oracle.normal_bf16(0xE3BD0000 + 1, nk * hkv * d))
@@ -715,6 +731,14 @@ def cpu_baseline(target_s=10.0):
             _, used = oracle.cpu_attention_f32(q, k, v, n_new, nk, hq, hkv, d, 1 / 16, th)
         return used
 
+    # the baseline computes the right thing: its output against the oracle on sampled rows
+    got, _ = oracle.cpu_attention_f32(q, k, v, n_new, nk, hq, hkv, d, 1 / 16, threads)
+    rows = np.arange(0, n_new, 7)  # query tokens
+    want = oracle.gqa_attention(oracle.f32_to_bf16(q), oracle.f32_to_bf16(k), oracle.f32_to_bf16(v), n_new, nk, hq,
+                                hkv, d, 1 / 16, rows=rows)
+    err = float(np.max(np.abs(got[rows] - want[rows])))
+    if err > 1e-4:
+        raise RuntimeError(f"CPU baseline output differs from the oracle by {err}")
     res = {}
     for th in sorted({threads, min(8, threads)}):
         step(th)  # warm
@@ -744,9 +768,112 @@ def cpu_baseline(target_s=10.0):
         "kind": "port",
         "sample": (f"{n} config-1 denoise steps (18 layers of 51x8 queries over 867 keys, d=256) "
                    f"with the oracle's fp32 ggml-order restatement on {used} OpenMP threads "
-                   f"(nproc={os.cpu_count()}, {cpu_model}); reference ggml b9016 is not available "
-                   f"offline; min(hw,8)={min(res)} threads: {res[min(res)][0]:.0f} us/step"),
+                   f"(nproc={os.cpu_count()}, the box's CPU share is 16 threads per GPU; {cpu_model}); "
+                   f"reference ggml b9016 is not available offline; min(hw,8)={min(res)} threads: "
+                   f"{res[min(res)][0]:.0f} us/step; output checked against the oracle on sampled rows "
+                   f"(max abs {err:.1e})"),
     }
+
+
+def _box_threads():
+    """Threads for the CPU baselines: the GPU box's CPU share is 16 threads per
+    GPU whatever nproc reports, so min(16, nproc)."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_baselines_other(cfgs, target_s=3.0):
+    """CPU restatements, in the reference's op order, of configs 2, 3 and 5 on the
+    host cores (each a bounded sample scaled to the full workload):
+      cfg2: 18 prefix layers of bidirectional 816x8 over 816 keys attention
+            (pi05.cpp:287-348: mul_mat -> soft_max_ext -> mul_mat, f32);
+      cfg3: one LingBot layer: slot allocation (LingBotKVCache update_meta_only,
+            lingbot_va.cpp:8793-8831, :8888-8902), scatter of the 1560-token chunk into the f32
+            [capacity][24][128] cache, gather of the 14040-slot window
+            (lingbot_flex_attn_cuda.cu:626-649, :875-898), dense attention of the
+            chunk over the window (:651-720) -- the attention on a sample of
+            query tokens, scaled;
+      cfg5: the W8 fallback order (cosmos3_w8_marlin_cuda.cu:157-186, :222-300):
+            dequantise the 3072x9216 int8 weight with its per-channel scale to f32,
+            then an f32 GEMM of the 1560x3072 activations."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    from threadpoolctl import threadpool_limits
+
+    th = _box_threads()
+    out = {}
+
+    def timed(fn, budget):
+        fn()
+        t0 = time.perf_counter()
+        n = 0
+        while True:
+            fn()
+            n += 1
+            if time.perf_counter() - t0 >= budget or n >= 50:
+                return (time.perf_counter() - t0) / n, n
+
+    if "cfg2" in cfgs:
+        n, hq, hkv, d, layers = 816, 8, 1, 256, 18
+        k = oracle.bf16_to_f32(oracle.normal_bf16(0xE3BD0002 + 1, n * hkv * d))
+        v = oracle.bf16_to_f32(oracle.normal_bf16(0xE3BD0002 + 2, n * hkv * d))
+        q = oracle.bf16_to_f32(oracle.normal_bf16(0xE3BD0002 + 10, n * hq * d))
+        sample_layers = 3
+        sec, reps = timed(lambda: [oracle.cpu_attention_f32(q, k, v, n, n, hq, hkv, d, 1 / 16, th)
+                                   for _ in range(sample_layers)], target_s)
+        out["cfg2"] = {"value": sec / sample_layers * layers * 1e6, "unit": "us per 18-layer prefill attention",
+                       "cores": th, "kind": "port",
+                       "sample": f"{reps} x {sample_layers} layers of 816x8 queries over 816 keys (d 256), "
+                                 f"fp32 oracle attention, scaled to 18 layers"}
+    if "cfg3" in cfgs:
+        cap, C_, H, d = 14040, 1560, 24, 128
+        g = np.random.default_rng(3)
+        cache_k = np.zeros((cap, H, d), np.float32)
+        cache_v = np.zeros_like(cache_k)
+        knew = g.standard_normal((C_, H, d), dtype=np.float32)
+        vnew = g.standard_normal((C_, H, d), dtype=np.float32)
+        sc = oracle.Cache(cap)
+        for _ in range(cap // C_):  # fill the window (cache mode 2: update_meta_only, :8888-8902)
+            sc.update_meta(C_, False)
+        slots_state = {}
+
+        def move():
+            slots = sc.update_meta(C_, False)  # evicts the oldest chunk
+            cache_k[slots] = knew
+            cache_v[slots] = vnew
+            valid = sc.collect_valid()
+            slots_state["k"] = cache_k[valid]
+            slots_state["v"] = cache_v[valid]
+        sec_move, reps_m = timed(move, target_s / 3)
+        kw, vw = slots_state["k"], slots_state["v"]
+        if kw.shape[0] != cap:
+            raise RuntimeError(f"cfg3 CPU baseline: window of {kw.shape[0]} slots, expected {cap}")
+        qs = 26  # query tokens sampled of the 1560
+        qq = g.standard_normal((qs, H, d), dtype=np.float32)
+        sec_att, reps_a = timed(lambda: oracle.cpu_attention_f32(qq, kw, vw, qs, cap, H, H, d, d ** -0.5, th),
+                                target_s * 2 / 3)
+        per_layer = sec_move + sec_att * C_ / qs
+        out["cfg3"] = {"value": per_layer * 1e6, "unit": "us per layer", "cores": th, "kind": "port",
+                       "sample": (f"slot allocation + f32 scatter of 1560x24x128 + gather of the 14040-slot window "
+                                  f"({sec_move * 1e6:.0f} us, {reps_m} runs, numpy single thread) + dense fp32 "
+                                  f"attention of {qs} of the 1560 query tokens over 14040 keys ({reps_a} runs), "
+                                  f"scaled by 1560/{qs}")}
+    if "cfg5" in cfgs:
+        M, K, N = 1560, 3072, 9216
+        g = np.random.default_rng(5)
+        w8 = g.integers(-127, 128, (K, N), dtype=np.int8)
+        scale = (g.random(N, dtype=np.float32) * 0.02 + 0.001).astype(np.float32)
+        x = oracle.bf16_to_f32(oracle.normal_bf16(0xE3BD0005, M * K)).reshape(M, K)
+
+        def gemm():
+            w = w8.astype(np.float32) * scale[None, :]  # dequantise to f32
+            return x @ w
+        with threadpool_limits(th):
+            sec, reps = timed(gemm, target_s)
+        out["cfg5"] = {"value": sec * 1e6, "unit": "us per 1560x3072->9216 projection", "cores": th,
+                       "kind": "port",
+                       "sample": f"{reps} full runs: numpy int8->f32 dequantisation with per-channel scales, "
+                                 f"then an f32 BLAS GEMM on {th} threads"}
+    return out
 
 
 TRAFFIC_FILE = "paged_attn_cfg1_traffic.md"
@@ -911,6 +1038,10 @@ def main():
         log("cpu baseline ...")
         cpu = cpu_baseline()
         log("cpu", json.dumps(cpu))
+        others = cpu_baselines_other(cfgs)
+        for name, r in others.items():
+            extra.setdefault(name, {})["cpu_baseline"] = r
+        log("cpu (other configs)", json.dumps(others))
 
     kern_us = r1["attn_us_avg_in_graph"]
     achieved = r1["attn_bytes_per_launch"] / (kern_us * 1e-6) / 1e9

@@ -8,6 +8,7 @@
 // here the free slots and the valid slots grouped by insertion id are kept in
 // ordered sets, so allocation and eviction touch only the slots they hand out.
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstring>
 #include <map>

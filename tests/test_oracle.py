@@ -701,3 +701,26 @@ def test_pbf16_attention_known_answers(orc):
     r = orc.pbf16_attention(qb, kb, vb, n_q, n_k, hq, hkv, D, 0.125)
     rel = np.abs(r - a).sum() / np.abs(a).sum()
     assert 1e-4 < rel < 3e-3, rel
+
+
+# ---------------- the CPU baseline's attention (bench.py cpu_baseline) ----------------
+@pytest.mark.parametrize("threads", [1, 4])
+def test_cpu_baseline_attention_matches_oracle(orc, threads):
+    # config-1 layer problem: 51 queries x 8 heads over 867 keys, one kv head, d 256
+    n_q, n_k, hq, hkv, d = 51, 867, 8, 1, 256
+    k = orc.normal_bf16(0xE3BD0001, n_k * hkv * d)
+    v = orc.normal_bf16(0xE3BD0002, n_k * hkv * d)
+    q = orc.normal_bf16(0xE3BD000A, n_q * hq * d)
+    got, used = orc.cpu_attention_f32(orc.bf16_to_f32(q), orc.bf16_to_f32(k), orc.bf16_to_f32(v), n_q, n_k, hq, hkv,
+                                      d, 1 / 16, threads)
+    assert used == threads
+    want = orc.gqa_attention(q, k, v, n_q, n_k, hq, hkv, d, 1 / 16)
+    assert np.allclose(got, want, rtol=0, atol=2e-5), np.max(np.abs(got - want))
+    # GQA: heads 0..3 read kv head 0, heads 4..7 kv head 1
+    n_k2, hkv2 = 100, 2
+    k2 = orc.normal_bf16(7, n_k2 * hkv2 * d)
+    v2 = orc.normal_bf16(8, n_k2 * hkv2 * d)
+    got2, _ = orc.cpu_attention_f32(orc.bf16_to_f32(q), orc.bf16_to_f32(k2), orc.bf16_to_f32(v2), n_q, n_k2, hq,
+                                    hkv2, d, 1 / 16, threads)
+    want2 = orc.gqa_attention(q, k2, v2, n_q, n_k2, hq, hkv2, d, 1 / 16)
+    assert np.allclose(got2, want2, rtol=0, atol=2e-5)
