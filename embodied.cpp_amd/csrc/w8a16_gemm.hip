@@ -19,21 +19,24 @@
 // with byte lane (k%2)*2 + (k/8)%2.  So for one column n the 16 k of a band sit
 // in the 4 words j = 0..3: word j holds k = 2j, 8+2j, 2j+1, 9+2j (bytes 0..3).
 //
-// MFMA mapping (32x32x16 bf16, C = X . W).  The B operand lane (column n, half
-// h) takes words j = 2h and 2h+1, i.e. k = {0,8,1,9,2,10,3,11} (h=0) or
-// {4,12,5,13,6,14,7,15} (h=1) of the band, in byte order.  The A operand (x)
-// is stored in LDS with the same k permutation inside every 16-k group, so the
-// two operands agree and no byte of W is moved twice.
+// MFMA mapping (32x32x16 bf16, C = X . W), natural k order in both operands:
+// lane half h of the A operand (row) and of the B operand (column n) holds k =
+// 8h .. 8h+7 of the 16-k step.  The staging thread holding words j = 2h', 2h'+1
+// of a column has k = 4h'..4h'+3 (bytes 0 and 2) and 8+4h'..11+4h' (bytes 1
+// and 3): it writes them dequantized to element 4h' of half 0 and of half 1.
+// x needs no reordering.
 //
-// Tiling.  A workgroup of 4 waves (2 x 2) computes a 256 x 128 tile of y; a
-// wave owns 128 x 64 (4 x 2 MFMA blocks, 128 accumulator registers).  Where
+// Tiling.  With bf16 x, K % 64 == 0 and 256-row tiles, the 256 x 256 kernel
+// further down (eight waves, x copied straight into LDS) runs.  Otherwise a
+// workgroup of 4 waves (2 x 2) computes a 256 x 128 tile of y; a wave owns
+// 128 x 64 (4 x 2 MFMA blocks, 128 accumulator registers).  Where
 // 256-row tiles would need no fewer rounds of resident workgroups, the tiles
 // are 128 x 128 instead (2 x 2 blocks a wave); each output element sums the
 // same k-steps in the same order either way.  K moves
 // in tiles of 64.  The next k-tile's x and W words are loaded into registers
-// while the current one is multiplied; they are then converted (x: permuted;
-// W: u8 -> bf16(u8 - 128), once per workgroup) and written to the single LDS
-// stage.  Two workgroups share a CU.
+// while the current one is multiplied; they are then converted (W: u8 ->
+// bf16(u8 - 128), once per workgroup) and written to the single LDS stage.
+// Two workgroups share a CU.
 //
 // Epilogue.  Plain mode writes y (bf16, or f32).  QKV mode splits the columns:
 // [0, n_q) go to a bf16 Q buffer, the next n_kv to the K pages and the last
@@ -99,42 +102,19 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
     return u >> 16;
 }
 
-// Four unsigned bytes of w -> bf16 bits of (byte - 128), two per dword.
-// 2^23 + b is built by byte permutation (0x4B000000 | b), the bias 2^23 + 128
-// subtracted in fp32 (exact), and the integer-valued result truncated to bf16
-// (exact: |b - 128| <= 128 has at most 8 significant bits).
-__device__ __forceinline__ void u8x4_to_bf16x4(uint32_t w, uint32_t &lo, uint32_t &hi) {
-    constexpr uint32_t MAGIC = 0x4B4B4B4Bu;
-    const float bias = 8388736.0f;  // 2^23 + 128
-    float f[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        // bytes [b_i, 0, 0, 0x4B]: selector picks byte i of w, two zeros, and 0x4B of MAGIC
-        const uint32_t sel = (uint32_t)(4 + i) | (0x0cu << 8) | (0x0cu << 16) | (0x03u << 24);
-        f[i] = __builtin_bit_cast(float, __builtin_amdgcn_perm(w, MAGIC, sel)) - bias;
-    }
-    // upper halves of two f32 -> one dword of two bf16
-    lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f[1]), __builtin_bit_cast(uint32_t, f[0]), 0x07060302u);
-    hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f[3]), __builtin_bit_cast(uint32_t, f[2]), 0x07060302u);
-}
 
-// Interleave two runs of 8 bf16 (k 0..7 in a, 8..15 in b) into the order
-// [0,8,1,9,...,7,15] the MFMA A operand uses inside a 16-k group.
-__device__ __forceinline__ void interleave16(const u32x4 &a, const u32x4 &b, u32x4 &o0, u32x4 &o1) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        // a[i] = (k 2i | k 2i+1 << 16), b[i] = (k 8+2i | k 9+2i << 16)
-        const uint32_t e0 = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);  // k 2i,  k 8+2i
-        const uint32_t e1 = __builtin_amdgcn_perm(b[i], a[i], 0x07060302u);  // k 2i+1, k 9+2i
-        if (i < 2) {
-            o0[2 * i] = e0;
-            o0[2 * i + 1] = e1;
-        } else {
-            o1[2 * (i - 2)] = e0;
-            o1[2 * (i - 2) + 1] = e1;
-        }
-    }
+// bf16 bits of (byte - 128) for byte i of w, in the upper half of a dword:
+// the integer-to-float conversion by exponent bias (a "magic number"): the
+// byte permute builds the f32 bit pattern 0x4B0000bb = 2^23 + b, subtracting
+// 2^23 + 128 in f32 is exact, and the integer result (|b - 128| <= 128, at most
+// 8 significant bits) is exactly the upper half of its f32 pattern.
+__device__ __forceinline__ uint32_t u8_bf16_hi(uint32_t w, int i) {
+    constexpr uint32_t MAGIC = 0x4B4B4B4Bu;
+    const uint32_t sel = (uint32_t)(4 + i) | (0x0cu << 8) | (0x0cu << 16) | (0x03u << 24);
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, __builtin_amdgcn_perm(w, MAGIC, sel)) - 8388736.0f);
 }
+// two bf16 (upper halves of a and b) -> one dword, a low
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
 template <bool XF32, int BM>
 struct Stage {
@@ -195,101 +175,48 @@ struct Stage {
         for (int i = 0; i < BM / 64; ++i) {
             const int u = tid + i * 256;
             const int row = u >> 2, g = u & 3;
-            u32x4 o0, o1;
-            interleave16(xa[i], xb[i], o0, o1);
-            uint16_t *dst = as + row * AS + g * 16;
-            *reinterpret_cast<u32x4 *>(dst) = o0;
-            *reinterpret_cast<u32x4 *>(dst + 8) = o1;
+            uint16_t *dst = as + row * AS + g * 16;  // natural k order
+            *reinterpret_cast<u32x4 *>(dst) = xa[i];
+            *reinterpret_cast<u32x4 *>(dst + 8) = xb[i];
         }
         const int band = tid >> 6, grp = (tid >> 5) & 1, idx = tid & 31;
         const int n8 = idx >> 2, q = idx & 3;
         const int h = q >> 1;
+        // natural k order: words 2h and 2h+1 of column n hold k 4h..4h+3
+        // (bytes 0, 2 of each) for half 0 and k 8+4h..11+4h (bytes 1, 3) for
+        // half 1, both at element 4h of the half
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int n = grp * 64 + ((q & 1) * 4 + e) * 8 + n8;  // column inside the tile
-            uint32_t o0, o1, o2, o3;
-            u8x4_to_bf16x4(w0[e], o0, o1);  // word j = 2h
-            u8x4_to_bf16x4(w1[e], o2, o3);  // word j = 2h + 1
-            const u32x4 o = {o0, o1, o2, o3};
-            const int slot = h ^ ((n >> 3) & 1);  // bank swizzle of the two halves
-            *reinterpret_cast<u32x4 *>(bs + ((band * BN + n) * 2 + slot) * 8) = o;
+            const uint32_t a0 = u8_bf16_hi(w0[e], 0), a1 = u8_bf16_hi(w0[e], 1), a2 = u8_bf16_hi(w0[e], 2),
+                           a3 = u8_bf16_hi(w0[e], 3);
+            const uint32_t b0 = u8_bf16_hi(w1[e], 0), b1 = u8_bf16_hi(w1[e], 1), b2 = u8_bf16_hi(w1[e], 2),
+                           b3 = u8_bf16_hi(w1[e], 3);
+            const int sw = (n >> 3) & 1;  // bank swizzle of the two halves
+            uint16_t *col = bs + (band * BN + n) * 16;
+            *reinterpret_cast<u32x2 *>(col + (0 ^ sw) * 8 + 4 * h) = u32x2{pack_hi(a0, a2), pack_hi(b0, b2)};
+            *reinterpret_cast<u32x2 *>(col + (1 ^ sw) * 8 + 4 * h) = u32x2{pack_hi(a1, a3), pack_hi(b1, b3)};
         }
     }
 };
 
-template <bool XF32, int MODE, int BM>
-__global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
-    __shared__ __attribute__((aligned(16))) uint16_t as[BM * AS];
-    __shared__ __attribute__((aligned(16))) uint16_t bs[B_ELEMS];
-
-    // XCD-aware order: consecutive logical tiles share an n-tile (the same
-    // W columns) and land on one XCD's L2.
-    const int nwg = (int)gridDim.x;
-    const int lin = (int)(blockIdx.x % 8) * (nwg / 8) + (int)(blockIdx.x / 8);
-    if (lin >= p.m_tiles * p.n_tiles) return;
-    const int mt = lin % p.m_tiles, nt = lin / p.m_tiles;
-    const int32_t m0 = mt * BM, n0 = nt * BN;
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int wm = wave >> 1, wn = wave & 1;
+// Epilogue of a wave's 128 (or 64) x 64 block: lane holds column n = n0 + wn*64 + j*32
+// + lrow and rows m0 + wm*(BM/2) + i*32 + (r/4)*8 + lhi*4 + r%4.  lds: at least BM*8 bytes
+// of LDS no wave reads any more (the QKV row table); NT threads in the workgroup.
+template <int MODE, int BM, int NT>
+__device__ __forceinline__ void gemm_epilogue(const GParams &p, f32x16 (&acc)[BM / 64][2], int32_t m0,
+                                              int32_t n0, int wm, int wn, int lane, uint16_t *lds) {
+    constexpr int MI = BM / 64;
     const int lrow = lane & 31, lhi = lane >> 5;
-
-    constexpr int MI = BM / 64;  // 32-row MFMA blocks a wave holds
-    f32x16 acc[MI][2];
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-    Stage<XF32, BM> st;
-    const int32_t n_kt = (p.K + BK - 1) / BK;
-    st.load(p, m0, n0, 0);
-    st.store(as, bs);
-    __syncthreads();
-
-    for (int32_t kt = 0; kt < n_kt; ++kt) {
-        const bool more = kt + 1 < n_kt;
-        if (more) st.load(p, m0, n0, (kt + 1) * BK);
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            bf16x8 a[4], bfr[2];
-#pragma unroll
-            for (int i = 0; i < MI; ++i) {
-                const int row = wm * (BM / 2) + i * 32 + lrow;
-                a[i] = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const u32x4 *>(as + row * AS + ks * 16 + lhi * 8));
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int n = wn * 64 + j * 32 + lrow;
-                const int slot = lhi ^ ((n >> 3) & 1);
-                bfr[j] = __builtin_bit_cast(bf16x8,
-                                            *reinterpret_cast<const u32x4 *>(bs + ((ks * BN + n) * 2 + slot) * 8));
-            }
-#pragma unroll
-            for (int i = 0; i < MI; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bfr[j], acc[i][j], 0, 0, 0);
-        }
-        if (more) {
-            __syncthreads();
-            st.store(as, bs);
-            __syncthreads();
-        }
-    }
-
-    // Epilogue: lane holds column n = n0 + wn*64 + j*32 + lrow and rows
-    // m0 + wm*128 + i*32 + (r/4)*8 + lhi*4 + r%4.
     if constexpr (MODE == Y_QKV) {
         // Row table in the (now free) A tile: for each of the tile's BM rows the
         // element offset of its page (page * hkv * 16 * head_dim) with the
         // in-page token in the low 4 bits, or -1 when the row is past M or its
         // slot is out of range or unmapped.  A page offset is a multiple of 16
         // elements, so its low 4 bits are free.
-        int64_t *rowtab = reinterpret_cast<int64_t *>(as);
+        int64_t *rowtab = reinterpret_cast<int64_t *>(lds);
         __syncthreads();  // every wave is past its last fragment read of as
-        for (int r = threadIdx.x; r < BM; r += 256) {
+        for (int r = threadIdx.x; r < BM; r += NT) {
             const int32_t m = m0 + r;
             int64_t e = -1;
             if (m < p.M) {
@@ -455,6 +382,309 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
     }
 }
 
+template <bool XF32, int MODE, int BM>
+__global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t as[BM * AS];
+    __shared__ __attribute__((aligned(16))) uint16_t bs[B_ELEMS];
+
+    // XCD-aware order: consecutive logical tiles share an n-tile (the same
+    // W columns) and land on one XCD's L2.
+    const int nwg = (int)gridDim.x;
+    const int lin = (int)(blockIdx.x % 8) * (nwg / 8) + (int)(blockIdx.x / 8);
+    if (lin >= p.m_tiles * p.n_tiles) return;
+    const int mt = lin % p.m_tiles, nt = lin / p.m_tiles;
+    const int32_t m0 = mt * BM, n0 = nt * BN;
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lrow = lane & 31, lhi = lane >> 5;
+
+    constexpr int MI = BM / 64;  // 32-row MFMA blocks a wave holds
+    f32x16 acc[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+    Stage<XF32, BM> st;
+    const int32_t n_kt = (p.K + BK - 1) / BK;
+    st.load(p, m0, n0, 0);
+    st.store(as, bs);
+    __syncthreads();
+
+    for (int32_t kt = 0; kt < n_kt; ++kt) {
+        const bool more = kt + 1 < n_kt;
+        if (more) st.load(p, m0, n0, (kt + 1) * BK);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            bf16x8 a[4], bfr[2];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int row = wm * (BM / 2) + i * 32 + lrow;
+                a[i] = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4 *>(as + row * AS + ks * 16 + lhi * 8));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = wn * 64 + j * 32 + lrow;
+                const int slot = lhi ^ ((n >> 3) & 1);
+                bfr[j] = __builtin_bit_cast(bf16x8,
+                                            *reinterpret_cast<const u32x4 *>(bs + ((ks * BN + n) * 2 + slot) * 8));
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bfr[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            __syncthreads();
+            st.store(as, bs);
+            __syncthreads();
+        }
+    }
+
+    gemm_epilogue<MODE, BM, 256>(p, acc, m0, n0, wm, wn, lane, as);
+}
+
+// ---- 256 x 256 tiles with x copied straight into LDS (bf16 x, K % 64 == 0) ----
+//
+// Eight waves (2 x 4), each the same 128 x 64 block as above, share a 256-row
+// x tile and a 256-column W tile, so each byte staged feeds twice the MFMAs of
+// the 256 x 128 tile.  Two LDS stages of 64 KB: while tile kt is multiplied,
+// tile kt + 1 is staged into the other one -- x by DMA (buffer_load ... lds,
+// no registers), W from registers loaded one tile earlier and dequantized on
+// the way.  W goes to LDS in natural k order ([band][n][half][8]: half h of
+// column n holds k = 8h .. 8h + 7), so x keeps its own order and needs no
+// permutation: lane (row, h) reads k-chunk 2 ks + h of its row, lane (n, h)
+// the same k of column n.  x rows are 128 bytes; the 16-byte chunk c of row r
+// sits at granule c ^ ((r >> 1) & 7) of the row, so the 16 rows a quarter-wave
+// reads hit 16 different bank groups (W: half h at slot h ^ ((n >> 3) & 1)).
+constexpr int TBN = 256;                        // tile columns
+constexpr int TX = 256 * BK;                    // bf16 elements of one x image
+constexpr int TW = (BK / 16) * TBN * 16;        // bf16 elements of one W image
+constexpr uint32_t RSRC_W3 = 0x00020000u;       // raw buffer, 32-bit elements
+
+__device__ __forceinline__ u32x4 buf_desc(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
+                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
+                 (uint32_t)__builtin_amdgcn_readfirstlane(bytes), RSRC_W3};
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+
+// Lane i's 16 bytes at byte offset voff of the buffer land at LDS byte m0 + 16 i
+// (bytes past the buffer's end land as zeros).  The kernel counts these loads
+// itself (wait_vmcnt).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const u32x4 &d, uint32_t m0, uint32_t voff) {
+    // every operand but voff is wave-uniform: pin it to SGPRs
+    const u32x4 desc = {(uint32_t)__builtin_amdgcn_readfirstlane(d[0]), (uint32_t)__builtin_amdgcn_readfirstlane(d[1]),
+                        (uint32_t)__builtin_amdgcn_readfirstlane(d[2]), (uint32_t)__builtin_amdgcn_readfirstlane(d[3])};
+    m0 = (uint32_t)__builtin_amdgcn_readfirstlane(m0);
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"  // SALU write of M0 -> LDS-DMA read of M0: one wait state
+        "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0),
+        "v"(voff), "s"(desc)
+        : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+
+// One thread's W words of a k-tile: thread t takes band t / 128 of the tile,
+// 64-column group (t / 32) % 4, and in it the words j = 2h, 2h + 1 (h = q / 2)
+// of the 4 columns with n % 8 = (t % 32) / 4 and (n / 8) % 8 = (q % 2) * 4 + e,
+// q = t % 4 (the layout recap at the top).  Loaded by inline asm, so the
+// kernel counts them with its copies (the compiler would wait for them with
+// vmcnt(0), i.e. for every copy issued after them too).
+struct WRegs {
+    u32x4 w0, w1;
+};
+
+__device__ __forceinline__ void load_w(WRegs &r, const GParams &p, int32_t n0, int32_t k0, int tid) {
+    const int band = tid >> 7, grp = (tid >> 5) & 3, idx = tid & 31;
+    const int n8 = idx >> 2, q = idx & 3;
+    const int c0 = n8 * 32 + (q & 1) * 4 + (q >> 1) * 16;
+    const int32_t kb = (k0 >> 4) + band;
+    // a group past N reads the last one instead (its columns are never stored)
+    const int32_t col64 = min((n0 >> 6) + grp, p.N / 64 - 1);
+    const uint32_t *src = p.qw + (int64_t)kb * (4 * (int64_t)p.N) + col64 * 256 + c0;
+    asm volatile(
+        "global_load_dwordx4 %0, %2, off\n\t"
+        "global_load_dwordx4 %1, %2, off offset:32"
+        : "=&v"(r.w0), "=&v"(r.w1)
+        : "v"(src)
+        : "memory");
+}
+
+// Column n holds, in word 2h, k = 4h, 8+4h, 4h+1, 9+4h and in word 2h+1
+// k = 4h+2, 10+4h, 4h+3, 11+4h (bytes 0..3): k 4h..4h+3 go to half 0 at
+// element 4h, k 8+4h..11+4h to half 1 at element 4h.  Part e: the e-th of the
+// thread's four columns.
+__device__ __forceinline__ void store_w_part(const WRegs &r, uint16_t *ws, int tid, int e) {
+    const int band = tid >> 7, grp = (tid >> 5) & 3, idx = tid & 31;
+    const int n8 = idx >> 2, q = idx & 3;
+    const int h = q >> 1;
+    const int n = grp * 64 + ((q & 1) * 4 + e) * 8 + n8;  // column inside the tile
+    const uint32_t a0 = u8_bf16_hi(r.w0[e], 0), a1 = u8_bf16_hi(r.w0[e], 1), a2 = u8_bf16_hi(r.w0[e], 2),
+                   a3 = u8_bf16_hi(r.w0[e], 3);
+    const uint32_t b0 = u8_bf16_hi(r.w1[e], 0), b1 = u8_bf16_hi(r.w1[e], 1), b2 = u8_bf16_hi(r.w1[e], 2),
+                   b3 = u8_bf16_hi(r.w1[e], 3);
+    const u32x2 lo = {pack_hi(a0, a2), pack_hi(b0, b2)};  // k 4h, 4h+1, 4h+2, 4h+3
+    const u32x2 hi = {pack_hi(a1, a3), pack_hi(b1, b3)};  // k 8+4h .. 11+4h
+    const int sw = (n >> 3) & 1;
+    uint16_t *col = ws + (band * TBN + n) * 16;
+    *reinterpret_cast<u32x2 *>(col + (0 ^ sw) * 8 + 4 * h) = lo;
+    *reinterpret_cast<u32x2 *>(col + (1 ^ sw) * 8 + 4 * h) = hi;
+}
+
+// vmcnt(N) that also re-defines the W registers, so no use of them is
+// scheduled before the wait.
+template <int N>
+__device__ __forceinline__ void wait_w(WRegs &r) {
+    static_assert(N >= 0 && N < 16, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(r.w0), "+v"(r.w1) : "n"(N));
+}
+
+// Pipeline, per k-tile kt: three x stages and two W stages.  At the top of
+// iteration kt the copies of x(kt+2) and the loads of W(kt+2) go out (into
+// the x stage and the register set nothing reads any more); the MFMAs of
+// tile kt run with the dequantized stores of W(kt+1) -- loaded a whole
+// iteration earlier -- between their k-steps; one counted wait for x(kt+1)
+// and W(kt+1), one barrier.
+constexpr int NXS = 3;
+
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void w8a16_gemm_tile256_kernel(GParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t smem[NXS * TX + 2 * TW];
+    constexpr int BM = 256, MI = 4;
+    const int nwg = (int)gridDim.x;
+    const int lin = (int)(blockIdx.x % 8) * (nwg / 8) + (int)(blockIdx.x / 8);
+    if (lin >= p.m_tiles * p.n_tiles) return;
+    const int mt = lin % p.m_tiles, nt = lin / p.m_tiles;
+    const int32_t m0 = mt * BM, n0 = nt * TBN;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = wave >> 2, wn = wave & 3;
+    const int lrow = lane & 31, lhi = lane >> 5;
+
+    // x rows [m0, M) as one buffer: rows past M read as zeros
+    const uint16_t *xb = reinterpret_cast<const uint16_t *>(p.x) + (int64_t)m0 * p.ldx;
+    const uint32_t xbytes = (uint32_t)min<int64_t>((int64_t)(p.M - m0) * p.ldx * 2, 0xffffffffLL);
+    const u32x4 xdesc = buf_desc(xb, xbytes);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
+    // copy i of this wave: granules (i*512 + wave*64 + lane) of the x image
+    uint32_t xoff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int g = i * 512 + wave * 64 + lane;
+        const int row = g >> 3, slot = g & 7;
+        const int c = slot ^ ((row >> 1) & 7);
+        xoff[i] = (uint32_t)((row * p.ldx + c * 8) * 2);
+    }
+    auto copy_x = [&](int stage, int32_t k0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            lds_copy16(xdesc, lds0 + (uint32_t)(stage * TX + i * 512 * 8 + wave * 64 * 8) * 2,
+                       xoff[i] + (uint32_t)k0 * 2);
+    };
+    uint16_t *const wst = smem + NXS * TX;  // the two W images
+
+    f32x16 acc[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+    const int32_t n_kt = p.K / BK;
+    WRegs wr[2];
+    copy_x(0, 0);
+    load_w(wr[0], p, n0, 0, tid);
+    if (n_kt > 1) {
+        copy_x(1, BK);
+        load_w(wr[1], p, n0, BK, tid);
+        wait_w<6>(wr[0]);
+    } else {
+        wait_w<0>(wr[0]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_w_part(wr[0], wst, tid, e);
+    __syncthreads();
+
+    // two iterations per trip so the W register set is a compile-time index
+    auto iteration = [&](int32_t kt, auto par) __attribute__((always_inline)) {
+        constexpr int P = decltype(par)::value;  // kt & 1
+        const int xs_cur = kt % NXS;
+        const bool issue = kt + 2 < n_kt;
+        const bool more = kt + 1 < n_kt;
+        if (issue) {
+            copy_x((kt + 2) % NXS, (kt + 2) * BK);
+            load_w(wr[P], p, n0, (kt + 2) * BK, tid);  // set P held W(kt), stored last iteration
+        }
+        const uint16_t *xs = smem + xs_cur * TX;
+        const uint16_t *ws = wst + P * TW;
+        uint16_t *ws_next = wst + (P ^ 1) * TW;
+        // fragments of k-step ks + 1 are read while the MFMAs of step ks run
+        bf16x8 fa[2][MI], fb[2][2];
+        auto read_frags = [&](int ks, int buf) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int row = wm * 128 + i * 32 + lrow;
+                const int c = ks * 2 + lhi;
+                fa[buf][i] = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4 *>(xs + (row * 8 + (c ^ ((row >> 1) & 7))) * 8));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = wn * 64 + j * 32 + lrow;
+                fb[buf][j] = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4 *>(ws + ((ks * TBN + n) * 2 + (lhi ^ ((n >> 3) & 1))) * 8));
+            }
+        };
+        read_frags(0, 0);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int cb = ks & 1;
+            if (ks + 1 < BK / 16) read_frags(ks + 1, cb ^ 1);
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][i], fb[cb][j], acc[i][j], 0, 0, 0);
+            if (more) {
+                if (ks == 0) {
+                    // x(kt+1) and W(kt+1) (issued before this iteration's copies) have landed
+                    if (issue)
+                        wait_w<6>(wr[P ^ 1]);
+                    else
+                        wait_w<0>(wr[P ^ 1]);
+                }
+                store_w_part(wr[P ^ 1], ws_next, tid, ks);
+            }
+        }
+        __syncthreads();
+    };
+    for (int32_t kt = 0; kt < n_kt; kt += 2) {
+        iteration(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < n_kt) iteration(kt + 1, std::integral_constant<int, 1>{});
+    }
+    gemm_epilogue<MODE, BM, 512>(p, acc, m0, n0, wm, wn, lane, smem);
+}
+
+template <int MODE>
+hipError_t launch_tile256(const GParams &p, hipStream_t stream) {
+    const int total = p.m_tiles * p.n_tiles;
+    const int grid = (total + 7) / 8 * 8;
+    hipLaunchKernelGGL((w8a16_gemm_tile256_kernel<MODE>), dim3(grid), dim3(512), 0, stream, p);
+    return hipGetLastError();
+}
+
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 // f32 [M][ldx] -> bf16 [M][K] (round to nearest even), four elements a thread.
@@ -534,7 +764,20 @@ int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
         p.ldx = p.K;
         xf32 = false;
     }
-    e = narrow ? dispatch<128>(p, xf32, mode, stream) : dispatch<256>(p, xf32, mode, stream);
+    if (!xf32 && p.K % BK == 0 && !narrow && aligned16(p.x)) {
+        // 256 x 256 tiles, x copied straight into LDS
+        p.n_tiles = (p.N + TBN - 1) / TBN;
+        p.m_tiles = (p.M + 255) / 256;
+        switch (mode) {
+            case Y_BF16: e = launch_tile256<Y_BF16>(p, stream); break;
+            case Y_F32_ROUNDED: e = launch_tile256<Y_F32_ROUNDED>(p, stream); break;
+            case Y_F32_RAW: e = launch_tile256<Y_F32_RAW>(p, stream); break;
+            case Y_GATED: e = launch_tile256<Y_GATED>(p, stream); break;
+            default: e = launch_tile256<Y_QKV>(p, stream); break;
+        }
+    } else {
+        e = narrow ? dispatch<128>(p, xf32, mode, stream) : dispatch<256>(p, xf32, mode, stream);
+    }
     if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "w8a16 launch: %s", hipGetErrorString(e));
     return EMB_OK;
 }
