@@ -34,6 +34,7 @@ sys.path.insert(0, str(ROOT / "embodied.cpp_amd"))
 
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 
 
 def log(*a):
@@ -668,6 +669,19 @@ def bench_cfg5(c: Ctx, steps, warmup):
     ms_op, _ = c.time_graph(oproj_many, max(2, steps // 4), 2)
     op_us = ms_op * 1e3 / k_launch
     op_flops = 2.0 * M * K * No
+    # the same O-projection on LingBot's dense resident weights (BF16, F32)
+    wb16 = torch.randn((No, K), dtype=torch.float32, device=c.dev).mul_(K ** -0.5).to(torch.bfloat16)
+    wf32 = wb16.float()
+    dense_us = {}
+    for name, wt, wty in (("bf16", wb16, emb.EMB_GGML_BF16), ("f32", wf32, emb.EMB_GGML_F32)):
+        def dense_many(st, wt=wt, wty=wty):
+            for _ in range(k_launch):
+                emb.dense_gated_residual(actx, wt, wty, M, K, No, xres, residual=xres, bias=ob,
+                                         gate=tproj[:, 2 * No:], ldg=6 * No, gate_bias=ssh[2 * No:3 * No],
+                                         x_bf16_workspace=xws if wty == emb.EMB_GGML_BF16 else None, stream=st)
+        ms_d, _ = c.time_graph(dense_many, max(2, steps // 4), 2)
+        dense_us[name] = ms_d * 1e3 / k_launch
+    del wb16, wf32
     nr_bytes = M * N * 2 + M * H * d * 2 + 2 * M * H * d * 2 + M * H * d * 2  # read QKV; write Q, K, V, V shadow
     gemm_bytes = M * K * 2 + K * N + N * 2 + M * N * 2
     return dict(norm_rope_append_us=ms_nr * 1e3 / k_launch,
@@ -680,7 +694,13 @@ def bench_cfg5(c: Ctx, steps, warmup):
                 lingbot_rownorm_rope_append_us=rn_us,
                 lingbot_rownorm_rope_append_gbs=rn_bytes / (rn_us * 1e-6) / 1e9,
                 oproj_gated_residual_us=op_us, oproj_gated_residual_tflops=op_flops / (op_us * 1e-6) / 1e12,
-                oproj_gated_residual_mfma_frac=op_flops / (op_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS)
+                oproj_gated_residual_mfma_frac=op_flops / (op_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS,
+                oproj_dense_bf16_us=dense_us["bf16"],
+                oproj_dense_bf16_tflops=op_flops / (dense_us["bf16"] * 1e-6) / 1e12,
+                oproj_dense_bf16_mfma_frac=op_flops / (dense_us["bf16"] * 1e-6) / 1e12 / PEAK_BF16_TFLOPS,
+                oproj_dense_f32_us=dense_us["f32"],
+                oproj_dense_f32_tflops=op_flops / (dense_us["f32"] * 1e-6) / 1e12,
+                oproj_dense_f32_mfma_frac=op_flops / (dense_us["f32"] * 1e-6) / 1e12 / PEAK_FP32_TFLOPS)
 
 
 class MT64:

@@ -70,7 +70,10 @@ constexpr int AS = BK + 8;  // bf16 elements per staged x row (bank spread)
 // A stage: BM x AS bf16; B stage:
 constexpr int B_ELEMS = (BK / 16) * BN * 2 * 8;  // [band][n][h][8] bf16
 
-enum { Y_BF16 = 0, Y_F32_ROUNDED = 1, Y_F32_RAW = 2, Y_QKV = 3, Y_GATED = 4 };
+enum { Y_BF16 = 0, Y_F32_ROUNDED = 1, Y_F32_RAW = 2, Y_QKV = 3, Y_GATED = 4, Y_GATED_B16 = 5, Y_GATED_F32 = 6 };
+// Y_GATED_B16: bf16 weights (ggml BF16 [N][K] rows), the fp32 accumulator
+// rounded to bf16 before the bias; Y_GATED_F32: f32 weights and f32 x, the
+// fp32 accumulator as is.  Both use the gated-residual epilogue without scales.
 
 struct GParams {
     const void *x;
@@ -93,6 +96,9 @@ struct GParams {
     // f32 x: when set, x is first rounded into this bf16 [M][K] buffer and the
     // GEMM reads that (the same bf16 values the in-kernel rounding gives)
     uint16_t *x_ws;
+    // dense weights (Y_GATED_B16: bf16, Y_GATED_F32: f32), row n at wd + n * ldw
+    const void *wd;
+    int64_t ldw;
 };
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
@@ -116,11 +122,13 @@ __device__ __forceinline__ uint32_t u8_bf16_hi(uint32_t w, int i) {
 // two bf16 (upper halves of a and b) -> one dword, a low
 __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
-template <bool XF32, int BM>
+template <bool XF32, int BM, bool WB16 = false>
 struct Stage {
-    // x: 4 units of (row, 16-k group); W: two 16-byte runs of one band.
+    // x: 4 units of (row, 16-k group); W: two 16-byte runs of one band
+    // (WB16: four 16-byte runs of bf16 weight rows).
     u32x4 xa[BM / 64], xb[BM / 64];
     u32x4 w0, w1;
+    u32x4 wr[WB16 ? 4 : 1];
 
     __device__ __forceinline__ void load(const GParams &p, int32_t m0, int32_t n0, int32_t k0) {
         const int tid = threadIdx.x;
@@ -151,6 +159,21 @@ struct Stage {
                 }
             }
         }
+        if constexpr (WB16) {
+            // unit u = t + 256 i: column n = u / 8 of the tile, 8 k (band u%8/2,
+            // half u%2) -- eight lanes read one row's 128 contiguous bytes
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int u = tid + i * 256;
+                const int n = u >> 3, sub = u & 7;
+                const int32_t k = k0 + sub * 8;
+                wr[i] = u32x4{0u, 0u, 0u, 0u};
+                if (n0 + n < p.N && k < p.K)
+                    wr[i] = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const uint16_t *>(p.wd) +
+                                                             (int64_t)(n0 + n) * p.ldw + k);
+            }
+            return;
+        }
         // W: thread t takes band t/64 of the tile, 64-column group (t/32)%2,
         // and the two 16-byte runs at word c0 and c0 + 8 of that group, where
         // c0 = (n%8)*32 + (q%2)*4 + (q/2)*16 for n%8 = (t%32)/4, q = t%4:
@@ -178,6 +201,17 @@ struct Stage {
             uint16_t *dst = as + row * AS + g * 16;  // natural k order
             *reinterpret_cast<u32x4 *>(dst) = xa[i];
             *reinterpret_cast<u32x4 *>(dst + 8) = xb[i];
+        }
+        if constexpr (WB16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int u = tid + i * 256;
+                const int n = u >> 3, sub = u & 7;
+                const int band = sub >> 1, h = sub & 1;
+                const int sw = (n >> 3) & 1;
+                *reinterpret_cast<u32x4 *>(bs + (band * BN + n) * 16 + (h ^ sw) * 8) = wr[i];
+            }
+            return;
         }
         const int band = tid >> 6, grp = (tid >> 5) & 1, idx = tid & 31;
         const int n8 = idx >> 2, q = idx & 3;
@@ -311,20 +345,25 @@ __device__ __forceinline__ void gemm_epilogue(const GParams &p, f32x16 (&acc)[BM
         store_cols(std::integral_constant<int, 1>{});
         return;
     }
-    if constexpr (MODE == Y_GATED) {
+    if constexpr (MODE == Y_GATED || MODE == Y_GATED_B16 || MODE == Y_GATED_F32) {
         // Per (row block i, column j): all 16 residual and gate loads first
         // (rows past M clamped to M - 1, so every load is in bounds and none
-        // waits on a branch), then the arithmetic and the stores.
+        // waits on a branch), then the arithmetic and the stores.  The dense
+        // modes have no scale and may have no residual (out = the projection,
+        // gated or not).
         auto body = [&](auto gated) __attribute__((always_inline)) {
 #pragma clang fp contract(off)
             constexpr bool G = decltype(gated)::value;
+            const bool R = p.res != nullptr;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int32_t n = n0 + wn * 64 + j * 32 + lrow;
                 if (n >= p.N) continue;
-                const float s = __builtin_bit_cast(float, (uint32_t)p.scales[(n >> 5) * 32 + ((n & 31) >> 3) * 2 +
-                                                                            ((n & 7) >> 1) * 8 + (n & 1)]
-                                                                 << 16);
+                float s = 1.0f;
+                if constexpr (MODE == Y_GATED)
+                    s = __builtin_bit_cast(float, (uint32_t)p.scales[(n >> 5) * 32 + ((n & 31) >> 3) * 2 +
+                                                                    ((n & 7) >> 1) * 8 + (n & 1)]
+                                                      << 16);
                 const float bn = p.bias ? p.bias[n] : 0.0f;
                 const float gb = G && p.gate_bias ? p.gate_bias[n] : 0.0f;
 #pragma unroll
@@ -333,16 +372,22 @@ __device__ __forceinline__ void gemm_epilogue(const GParams &p, f32x16 (&acc)[BM
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int32_t m = min(m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3), p.M - 1);
-                        rv[r] = p.res[(int64_t)m * p.ldr + n];
+                        rv[r] = R ? p.res[(int64_t)m * p.ldr + n] : 0.0f;
                         if constexpr (G) gv[r] = p.gate[(int64_t)m * p.ldg + n];
                     }
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int32_t m = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 + lhi * 4 + (r & 3);
-                        float a = acc[i][j][r] * s;
+                        float a;
+                        if constexpr (MODE == Y_GATED)
+                            a = acc[i][j][r] * s;
+                        else if constexpr (MODE == Y_GATED_B16)
+                            a = __builtin_bit_cast(float, f32_to_bf16_bits(acc[i][j][r]) << 16);
+                        else
+                            a = acc[i][j][r];
                         if (p.bias) a = a + bn;
                         if constexpr (G) a = a * (gv[r] + gb);
-                        float v = rv[r] + a;
+                        float v = R ? rv[r] + a : a;
                         if (p.round_out) v = __builtin_bit_cast(float, f32_to_bf16_bits(v) << 16);
                         if (m < p.M) reinterpret_cast<float *>(p.y)[(int64_t)m * p.ldy + n] = v;
                     }
@@ -406,7 +451,7 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-    Stage<XF32, BM> st;
+    Stage<XF32, BM, MODE == Y_GATED_B16> st;
     const int32_t n_kt = (p.K + BK - 1) / BK;
     st.load(p, m0, n0, 0);
     st.store(as, bs);
@@ -445,6 +490,94 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GParams p) {
     }
 
     gemm_epilogue<MODE, BM, 256>(p, acc, m0, n0, wm, wn, lane, as);
+}
+
+// ---- f32 weights and f32 x: fp32 MFMA (32x32x2) ----
+//
+// The ggml F32 x F32 product (cublasSgemm in the CUDA backend): products and
+// sums in fp32, nothing rounded to a narrower type.  A workgroup of 4 waves
+// (2 x 2) computes a 128 x 128 tile, 64 x 64 a wave (2 x 2 blocks), K in tiles
+// of 32 staged through registers into one LDS stage.  One MFMA takes a k pair:
+// lane (row, h) supplies A[row][k] with k = 2s + h at step s.  Both operands
+// read 16 bytes a lane at k = 8q + 4h .. 8q + 4h + 3 and step 4q + t uses the
+// t-th of them, so the k sum runs in one fixed permuted order for A and W.
+constexpr int FBM = 128, FBK = 32, FLD = FBK + 4;  // rows padded by 16 bytes
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void f32_gemm_kernel(GParams p) {
+    __shared__ __attribute__((aligned(16))) float xs[FBM * FLD];
+    __shared__ __attribute__((aligned(16))) float ws[FBM * FLD];
+    const int nwg = (int)gridDim.x;
+    const int lin = (int)(blockIdx.x % 8) * (nwg / 8) + (int)(blockIdx.x / 8);
+    if (lin >= p.m_tiles * p.n_tiles) return;
+    const int mt = lin % p.m_tiles, nt = lin / p.m_tiles;
+    const int32_t m0 = mt * FBM, n0 = nt * FBM;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lrow = lane & 31, lhi = lane >> 5;
+    const float *xg = reinterpret_cast<const float *>(p.x);
+    const float *wg = reinterpret_cast<const float *>(p.wd);
+
+    // unit u = t + 256 i: row u / 8 of the tile, k = 4 (u % 8) of the k-tile
+    f32x4 rx[4], rw[4];
+    auto load = [&](int32_t k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int u = tid + i * 256;
+            const int row = u >> 3;
+            const int32_t k = k0 + (u & 7) * 4;
+            rx[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            rw[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (m0 + row < p.M && k < p.K) rx[i] = *reinterpret_cast<const f32x4 *>(xg + (int64_t)(m0 + row) * p.ldx + k);
+            if (n0 + row < p.N && k < p.K) rw[i] = *reinterpret_cast<const f32x4 *>(wg + (int64_t)(n0 + row) * p.ldw + k);
+        }
+    };
+    auto store = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int u = tid + i * 256;
+            const int off = (u >> 3) * FLD + (u & 7) * 4;
+            *reinterpret_cast<f32x4 *>(xs + off) = rx[i];
+            *reinterpret_cast<f32x4 *>(ws + off) = rw[i];
+        }
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    const int32_t n_kt = (p.K + FBK - 1) / FBK;
+    load(0);
+    store();
+    __syncthreads();
+    for (int32_t kt = 0; kt < n_kt; ++kt) {
+        const bool more = kt + 1 < n_kt;
+        if (more) load((kt + 1) * FBK);
+#pragma unroll
+        for (int q = 0; q < FBK / 8; ++q) {
+            f32x4 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const f32x4 *>(xs + (wm * 64 + i * 32 + lrow) * FLD + 8 * q + 4 * lhi);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const f32x4 *>(ws + (wn * 64 + j * 32 + lrow) * FLD + 8 * q + 4 * lhi);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][t], b[j][t], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            __syncthreads();
+            store();
+            __syncthreads();
+        }
+    }
+    gemm_epilogue<MODE, FBM, 256>(p, acc, m0, n0, wm, wn, lane, reinterpret_cast<uint16_t *>(xs));
 }
 
 // ---- 256 x 256 tiles with x copied straight into LDS (bf16 x, K % 64 == 0) ----
@@ -719,6 +852,7 @@ hipError_t dispatch(const GParams &p, bool xf32, int mode, hipStream_t stream) {
             case Y_F32_ROUNDED: return launch<true, Y_F32_ROUNDED, BM>(p, stream);
             case Y_F32_RAW: return launch<true, Y_F32_RAW, BM>(p, stream);
             case Y_GATED: return launch<true, Y_GATED, BM>(p, stream);
+            case Y_GATED_B16: return launch<true, Y_GATED_B16, BM>(p, stream);
             default: return launch<true, Y_QKV, BM>(p, stream);
         }
     }
@@ -727,18 +861,44 @@ hipError_t dispatch(const GParams &p, bool xf32, int mode, hipStream_t stream) {
         case Y_F32_ROUNDED: return launch<false, Y_F32_ROUNDED, BM>(p, stream);
         case Y_F32_RAW: return launch<false, Y_F32_RAW, BM>(p, stream);
         case Y_GATED: return launch<false, Y_GATED, BM>(p, stream);
+        case Y_GATED_B16: return launch<false, Y_GATED_B16, BM>(p, stream);
         default: return launch<false, Y_QKV, BM>(p, stream);
     }
 }
 
-int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
-    EMB_CHECK_ARG(p.x && p.qw && p.scales, "null x/qweight/scales");
+// f32 weights: 128 x 128 tiles of the fp32 MFMA kernel
+int run_gemm_f32(GParams p, hipStream_t stream) {
+    EMB_CHECK_ARG(p.x && p.wd, "null x/weight");
     EMB_CHECK_ARG(p.M > 0 && p.K > 0 && p.N > 0, "non-positive size");
-    if (p.K % 16 != 0 || p.N % 64 != 0)
+    if (p.K % 4 != 0)
+        return emb::set_error(EMB_ERR_UNSUPPORTED, "f32 weights need in_features %% 4 == 0 (got %d)", p.K);
+    EMB_CHECK_ARG(p.ldx >= p.K && p.ldx % 4 == 0 && p.ldw >= p.K && p.ldw % 4 == 0,
+                  "x and weight row strides must cover K, 16-byte aligned");
+    EMB_CHECK_ARG(aligned16(p.x) && aligned16(p.wd), "x and weight must be 16-byte aligned");
+    p.m_tiles = (p.M + FBM - 1) / FBM;
+    p.n_tiles = (p.N + FBM - 1) / FBM;
+    EMB_CHECK_ARG((int64_t)p.m_tiles * p.n_tiles < INT_MAX / 2, "problem too large");
+    const int total = p.m_tiles * p.n_tiles;
+    hipLaunchKernelGGL((f32_gemm_kernel<Y_GATED_F32>), dim3((total + 7) / 8 * 8), dim3(256), 0, stream, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "f32 GEMM launch: %s", hipGetErrorString(e));
+    return EMB_OK;
+}
+
+int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
+    const bool dense = mode == Y_GATED_B16;
+    EMB_CHECK_ARG(p.x && (dense ? p.wd != nullptr : p.qw && p.scales), "null x/weights/scales");
+    EMB_CHECK_ARG(p.M > 0 && p.K > 0 && p.N > 0, "non-positive size");
+    if (dense) {
+        if (p.K % 16 != 0)
+            return emb::set_error(EMB_ERR_UNSUPPORTED, "bf16 weights need in_features %% 16 == 0 (got %d)", p.K);
+        EMB_CHECK_ARG(p.ldw >= p.K && p.ldw % 8 == 0 && aligned16(p.wd),
+                      "weight rows must cover K, 16-byte aligned");
+    } else if (p.K % 16 != 0 || p.N % 64 != 0)
         return emb::set_error(EMB_ERR_UNSUPPORTED, "W8A16 needs in_features %% 16 == 0 and out_features %% 64 == 0 "
                                                    "(got %d, %d)", p.K, p.N);
     EMB_CHECK_ARG(p.ldx >= p.K && (p.ldx * (xf32 ? 4 : 2)) % 16 == 0, "x row stride must cover K, 16-byte aligned");
-    EMB_CHECK_ARG(aligned16(p.x) && aligned16(p.qw), "x and qweight must be 16-byte aligned");
+    EMB_CHECK_ARG(aligned16(p.x) && (dense || aligned16(p.qw)), "x and qweight must be 16-byte aligned");
     EMB_CHECK_ARG((int64_t)p.M * (p.N / 64) < INT_MAX, "problem too large");
     // Tile height by rounds of resident workgroups on MI355X's 256 CUs: two
     // 256-row workgroups fit a CU (VGPRs), three 128-row ones.  A 128-row
@@ -764,7 +924,7 @@ int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
         p.ldx = p.K;
         xf32 = false;
     }
-    if (!xf32 && p.K % BK == 0 && !narrow && aligned16(p.x)) {
+    if (!dense && !xf32 && p.K % BK == 0 && !narrow && aligned16(p.x)) {
         // 256 x 256 tiles, x copied straight into LDS
         p.n_tiles = (p.N + TBN - 1) / TBN;
         p.m_tiles = (p.M + 255) / 256;
@@ -797,6 +957,59 @@ int check_ref_shapes(int batch, int in_features, int out_features, int qweight_r
 __global__ void f32_to_bf16_kernel(const float *x, uint16_t *y, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         y[i] = (uint16_t)f32_to_bf16_bits(x[i]);
+}
+
+// Argument checks and parameters shared by the gated-residual entry points.
+// residual may be NULL here (the dense entry's plain projection); out may be
+// the residual itself (each element is read, then written, by one thread);
+// any other overlap of out with an input is rejected, and so is a bf16
+// workspace that overlaps anything the GEMM reads or writes after filling it.
+int gated_params(GParams &p, const void *x, int32_t x_is_f32, int64_t ldx, int32_t M, int32_t K, int32_t N,
+                 const float *bias, const float *gate, int64_t ldg, const float *gate_bias, const float *residual,
+                 int64_t ldr, float *out, int64_t ldo, int32_t round_bf16, void *x_bf16_workspace) {
+    EMB_CHECK_ARG(out, "null out");
+    EMB_CHECK_ARG(M > 0 && K > 0 && N > 0, "non-positive size");
+    EMB_CHECK_ARG((!residual || ldr >= N) && ldo >= N, "ldr and ldo must cover N");
+    EMB_CHECK_ARG(!gate || ldg >= N, "ldg must cover N");
+    EMB_CHECK_ARG(gate || !gate_bias, "gate_bias needs a gate");
+    const float *olo = out, *ohi = out + (int64_t)(M - 1) * ldo + N;
+    auto overlaps = [&](const void *q, int64_t bytes) {
+        const char *a = (const char *)q, *b = a + bytes;
+        return q && a < (const char *)ohi && (const char *)olo < b;
+    };
+    EMB_CHECK_ARG(!residual || residual == out || !overlaps(residual, ((int64_t)(M - 1) * ldr + N) * 4),
+                  "out overlaps residual without being it");
+    EMB_CHECK_ARG(!overlaps(gate, gate ? ((int64_t)(M - 1) * ldg + N) * 4 : 0) && !overlaps(bias, (int64_t)N * 4) &&
+                      !overlaps(gate_bias, (int64_t)N * 4),
+                  "out overlaps gate or bias");
+    EMB_CHECK_ARG(residual != out || ldr == ldo, "in-place update needs ldr == ldo");
+    if (x_is_f32 && x_bf16_workspace) {  // the workspace is written before the GEMM reads the others
+        const char *w0 = (const char *)x_bf16_workspace, *w1 = w0 + (int64_t)M * K * 2;
+        auto hits = [&](const void *q, int64_t bytes) {
+            return q && (const char *)q < w1 && w0 < (const char *)q + bytes;
+        };
+        EMB_CHECK_ARG(!hits(out, ((int64_t)(M - 1) * ldo + N) * 4) &&
+                          !hits(residual, residual ? ((int64_t)(M - 1) * ldr + N) * 4 : 0) &&
+                          !hits(gate, gate ? ((int64_t)(M - 1) * ldg + N) * 4 : 0) && !hits(bias, (int64_t)N * 4) &&
+                          !hits(gate_bias, (int64_t)N * 4) && !hits(x, ((int64_t)(M - 1) * ldx + K) * 4),
+                      "x_bf16_workspace overlaps an input or out");
+    }
+    p.x = x;
+    p.ldx = ldx;
+    p.M = M;
+    p.K = K;
+    p.N = N;
+    p.y = out;
+    p.ldy = ldo;
+    p.bias = bias;
+    p.gate = gate;
+    p.gate_bias = gate_bias;
+    p.res = residual;
+    p.ldg = ldg;
+    p.ldr = ldr;
+    p.round_out = round_bf16 != 0;
+    p.x_ws = (uint16_t *)x_bf16_workspace;
+    return EMB_OK;
 }
 
 }  // namespace
@@ -857,53 +1070,42 @@ int emb_w8a16_gated_residual(const void *x, int32_t x_is_f32, int64_t ldx, const
                              const float *gate, int64_t ldg, const float *gate_bias, const float *residual,
                              int64_t ldr, float *out, int64_t ldo, int32_t round_bf16, void *x_bf16_workspace,
                              hipStream_t stream) {
-    EMB_CHECK_ARG(residual && out, "null residual/out");
-    EMB_CHECK_ARG(M > 0 && K > 0 && N > 0, "non-positive size");
-    EMB_CHECK_ARG(ldr >= N && ldo >= N, "ldr and ldo must cover N");
-    EMB_CHECK_ARG(!gate || ldg >= N, "ldg must cover N");
-    EMB_CHECK_ARG(gate || !gate_bias, "gate_bias needs a gate");
-    // out may be the residual itself (each element is read, then written, by
-    // one thread); any other overlap of out with an input is rejected
-    const float *olo = out, *ohi = out + (int64_t)(M - 1) * ldo + N;
-    auto overlaps = [&](const void *q, int64_t bytes) {
-        const char *a = (const char *)q, *b = a + bytes;
-        return q && a < (const char *)ohi && (const char *)olo < b;
-    };
-    EMB_CHECK_ARG(residual == out || !overlaps(residual, ((int64_t)(M - 1) * ldr + N) * 4),
-                  "out overlaps residual without being it");
-    EMB_CHECK_ARG(!overlaps(gate, gate ? ((int64_t)(M - 1) * ldg + N) * 4 : 0) && !overlaps(bias, (int64_t)N * 4) &&
-                      !overlaps(gate_bias, (int64_t)N * 4),
-                  "out overlaps gate or bias");
-    EMB_CHECK_ARG(residual != out || ldr == ldo, "in-place update needs ldr == ldo");
-    if (x_is_f32 && x_bf16_workspace) {  // the workspace is written before the GEMM reads the others
-        const char *w0 = (const char *)x_bf16_workspace, *w1 = w0 + (int64_t)M * K * 2;
-        auto hits = [&](const void *q, int64_t bytes) {
-            return q && (const char *)q < w1 && w0 < (const char *)q + bytes;
-        };
-        EMB_CHECK_ARG(!hits(out, ((int64_t)(M - 1) * ldo + N) * 4) && !hits(residual, ((int64_t)(M - 1) * ldr + N) * 4) &&
-                          !hits(gate, gate ? ((int64_t)(M - 1) * ldg + N) * 4 : 0) && !hits(bias, (int64_t)N * 4) &&
-                          !hits(gate_bias, (int64_t)N * 4) && !hits(x, ((int64_t)(M - 1) * ldx + K) * 4),
-                      "x_bf16_workspace overlaps an input or out");
-    }
+    EMB_CHECK_ARG(residual, "null residual");
     GParams p{};
-    p.x = x;
-    p.ldx = ldx;
+    const int rc = gated_params(p, x, x_is_f32, ldx, M, K, N, bias, gate, ldg, gate_bias, residual, ldr, out, ldo,
+                                round_bf16, x_bf16_workspace);
+    if (rc) return rc;
     p.qw = reinterpret_cast<const uint32_t *>(qweight);
     p.scales = scales;
-    p.M = M;
-    p.K = K;
-    p.N = N;
-    p.y = out;
-    p.ldy = ldo;
-    p.bias = bias;
-    p.gate = gate;
-    p.gate_bias = gate_bias;
-    p.res = residual;
-    p.ldg = ldg;
-    p.ldr = ldr;
-    p.round_out = round_bf16 != 0;
-    p.x_ws = (uint16_t *)x_bf16_workspace;
     return run_gemm(p, x_is_f32 != 0, Y_GATED, stream);
+}
+
+int emb_dense_gated_residual(const void *x, int32_t x_is_f32, int64_t ldx, const void *weight, int32_t weight_type,
+                             int64_t ldw, int32_t M, int32_t K, int32_t N, const float *bias, const float *gate,
+                             int64_t ldg, const float *gate_bias, const float *residual, int64_t ldr, float *out,
+                             int64_t ldo, int32_t round_bf16, void *x_bf16_workspace, hipStream_t stream) {
+    EMB_CHECK_ARG(weight, "null weight");
+    if (weight_type != EMB_GGML_BF16 && weight_type != EMB_GGML_F32)
+        return emb::set_error(EMB_ERR_UNSUPPORTED, "weight_type must be ggml BF16 (30) or F32 (0), got %d",
+                              weight_type);
+    if (weight_type == EMB_GGML_F32 && !x_is_f32)
+        return emb::set_error(EMB_ERR_UNSUPPORTED, "f32 weights take f32 x");
+    const bool f32w = weight_type == EMB_GGML_F32;
+    EMB_CHECK_ARG(ldw >= K, "ldw must cover K");
+    // the weights are read while out is written: no overlap
+    if (out && M > 0 && N > 0 && ldo >= N) {
+        const char *w0 = (const char *)weight, *w1 = w0 + ((int64_t)(N - 1) * ldw + K) * (f32w ? 4 : 2);
+        const char *o0 = (const char *)out, *o1 = (const char *)(out + (int64_t)(M - 1) * ldo + N);
+        EMB_CHECK_ARG(!(w0 < o1 && o0 < w1), "out overlaps the weights");
+    }
+    GParams p{};
+    const int rc = gated_params(p, x, x_is_f32, ldx, M, K, N, bias, gate, ldg, gate_bias, residual, ldr, out, ldo,
+                                round_bf16, f32w ? nullptr : x_bf16_workspace);
+    if (rc) return rc;
+    p.wd = weight;
+    p.ldw = ldw;
+    if (f32w) return run_gemm_f32(p, stream);
+    return run_gemm(p, x_is_f32 != 0, Y_GATED_B16, stream);
 }
 
 // ---- reference-named face (kernels/cosmos3/cosmos3_w8_marlin_cuda.h:24-84) ----

@@ -152,6 +152,9 @@ _SIGS = {
     "emb_w8a16_gated_residual": (C.c_int, [vp, C.c_int32, C.c_int64, vp, vp, C.c_int32, C.c_int32,
                                            C.c_int32, vp, vp, C.c_int64, vp, vp, C.c_int64, vp,
                                            C.c_int64, C.c_int32, vp, vp]),
+    "emb_dense_gated_residual": (C.c_int, [vp, C.c_int32, C.c_int64, vp, C.c_int32, C.c_int64, C.c_int32,
+                                           C.c_int32, C.c_int32, vp, vp, C.c_int64, vp, vp, C.c_int64, vp,
+                                           C.c_int64, C.c_int32, vp, vp]),
     "cosmos3_w8a16_linear_f32": (C.c_int, [vp, vp, vp, vp] + [C.c_int] * 7 + [vp]),
     "cosmos3_w8a16_linear_f32_ws": (C.c_int, [vp] * 8 + [C.c_int] * 7 + [vp]),
     "cosmos3_w8a16_linear_bf16_ws": (C.c_int, [vp] * 7 + [C.c_int] * 7 + [vp]),
@@ -538,6 +541,29 @@ def w8a16_gated_residual(x, qweight, scales, M, K, N, residual, out, bias=None, 
                                                 ptr(out), ldo or N, int(round_bf16),
                                                 ptr(x_bf16_workspace), stream_ptr(stream)),
                  "emb_w8a16_gated_residual")
+
+
+def dense_gated_residual(x, weight, weight_type, M, K, N, out, residual=None, bias=None, gate=None,
+                         gate_bias=None, ldw=None, ldg=None, ldr=None, ldo=None, round_bf16=False,
+                         x_is_f32=True, ldx=None, x_bf16_workspace=None, stream=None):
+    """out = [residual +] (lin(x) [* (gate + gate_bias)]) with ggml dense
+    weights, lin = W x + bias in ggml's CUDA mul_mat numerics
+    (emb_dense_gated_residual); weight_type EMB_GGML_BF16 or EMB_GGML_F32."""
+    wsz = 4 if weight_type == EMB_GGML_F32 else 2
+    _need_rows(x, M, ldx or K, K, 4 if x_is_f32 else 2, "x")
+    _need_rows(weight, N, ldw or K, K, wsz, "weight")
+    _need_rows(residual, M, ldr or N, N, 4, "residual")
+    _need_rows(out, M, ldo or N, N, 4, "out")
+    _need_rows(gate, M, ldg or N, N, 4, "gate")
+    _need_bytes(bias, N * 4, "bias")
+    _need_bytes(gate_bias, N * 4, "gate_bias")
+    if x_is_f32:
+        _need_bytes(x_bf16_workspace, M * K * 2, "x_bf16_workspace")
+    return check(lib().emb_dense_gated_residual(ptr(x), int(x_is_f32), ldx or K, ptr(weight), int(weight_type),
+                                                ldw or K, M, K, N, ptr(bias), ptr(gate), ldg or N,
+                                                ptr(gate_bias), ptr(residual), ldr or N, ptr(out), ldo or N,
+                                                int(round_bf16), ptr(x_bf16_workspace), stream_ptr(stream)),
+                 "emb_dense_gated_residual")
 
 
 def attn_workspace_bytes(batch, max_q, hq, hkv, d, splits):

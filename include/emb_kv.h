@@ -587,6 +587,31 @@ int emb_w8a16_gated_residual(const void *x, int32_t x_is_f32, int64_t ldx, const
                              int64_t ldo, int32_t round_bf16, void *x_bf16_workspace,
                              hipStream_t stream);
 
+/* The same projection with the block's resident weights in ggml's dense
+ * layouts (models/lingbot_va.cpp:1808-1851: F32 by default, BF16 by
+ * VLA_LINGBOT_RESIDENT_BLOCK_DTYPE), replacing lin(o, self_ctx) =
+ * ggml_add(ggml_mul_mat(W, x), bias) (:1178-1180) and the gated residual
+ * (:11693-11695) with the product in the numerics of ggml's CUDA mul_mat:
+ *   weight_type EMB_GGML_BF16: W bf16 [N][ldw]; x (f32, rounded to bf16, or
+ *     bf16) times W with fp32 accumulation, the result rounded to bf16 and
+ *     widened (the cuBLAS bf16 GEMM and its bf16 -> f32 conversion), then
+ *     + bias; x_bf16_workspace as for emb_w8a16_gated_residual;
+ *   weight_type EMB_GGML_F32: W f32 [N][ldw], x f32; an fp32 product (the
+ *     reference's cublasSgemm), + bias; no workspace.
+ *   out[m][n] = residual[m][n] + lin[m][n] * (gate[m][n] + gate_bias[n])
+ * with each operation rounded to f32 separately.  residual NULL: out = lin *
+ * (gate + gate_bias), or out = lin with no gate (the plain lin() of any
+ * LingBot projection).  Other arguments as emb_w8a16_gated_residual; W must
+ * not overlap out.  Needs K % 16 == 0 (BF16) or K % 4 == 0 (F32), rows
+ * 16-byte aligned.  ggml's quantized block types are not taken
+ * (EMB_ERR_UNSUPPORTED). */
+int emb_dense_gated_residual(const void *x, int32_t x_is_f32, int64_t ldx, const void *weight,
+                             int32_t weight_type, int64_t ldw, int32_t M, int32_t K, int32_t N,
+                             const float *bias, const float *gate, int64_t ldg,
+                             const float *gate_bias, const float *residual, int64_t ldr, float *out,
+                             int64_t ldo, int32_t round_bf16, void *x_bf16_workspace,
+                             hipStream_t stream);
+
 /* Reference-named W8 face (kernels/cosmos3/cosmos3_w8_marlin_cuda.h:24-84 with
  * hipStream_t).  y is f32 holding the bf16-rounded result.  linear_f32_ws
  * rounds x into x_bf16_workspace (batch * in_features bf16, or NULL: rounded

@@ -343,7 +343,8 @@ def gated_residual(y, residual, bias=None, gate=None, gate_bias=None, round_bf16
     (models/lingbot_va.cpp:11693-11695, lin() :1178-1180, bf16 boundary
     :11676-11678): a1 = y + bias; x = residual + a1 * (gate + gate_bias), every
     node an f32 operation of its own.  y is the projection's f32 value ([M][N],
-    e.g. the second result of w8a16_gemm); gate [M][N] or None."""
+    e.g. the second result of w8a16_gemm); gate [M][N] or None; residual None
+    leaves x = a1 * (gate + gate_bias) (or a1)."""
     f = np.float32
     a = np.asarray(y, f)
     if bias is not None:
@@ -353,10 +354,41 @@ def gated_residual(y, residual, bias=None, gate=None, gate_bias=None, round_bf16
         if gate_bias is not None:
             g = (g + np.asarray(gate_bias, f)[None, :]).astype(f)
         a = (a * g).astype(f)
-    out = (np.asarray(residual, f) + a).astype(f)
+    out = a if residual is None else (np.asarray(residual, f) + a).astype(f)
     if round_bf16:
         out = bf16_to_f32(f32_to_bf16(out))
     return out
+
+
+def dense_linear(x, w, bf16_weights, bias=None, rows=None):
+    """lin(w, x) = ggml_add(ggml_mul_mat(w, x), bias) of the LingBot graph
+    (models/lingbot_va.cpp:1178-1180) for its dense resident weight types
+    (:1808-1851), in the numerics of ggml's CUDA mul_mat (ggml b9016, a
+    dependency not vendored in the reference: ggml_cuda_op_mul_mat_cublas).
+      bf16_weights: x rounded to bf16 (RNE), times the bf16 weights with an
+        fp32 accumulator (cublasGemmEx, CUBLAS_COMPUTE_32F) into a bf16
+        result, widened to f32;
+      otherwise: an f32 product (cublasSgemm).
+    The accumulation order of cuBLAS is unspecified; the exact sum stands for
+    it, taken in float64 (bf16 and f32 products are exact there), rounded to
+    f32, then (bf16 weights) to bf16.  x f32 [M][K] (or bf16 bits with
+    bf16 weights), w [N][K] (ggml row order: ne0 = K) as f32 or bf16 bits;
+    bias f32 [N] added as its own f32 node.  rows: the x rows to evaluate."""
+    f = np.float32
+    x = np.asarray(x)
+    if rows is not None:
+        x = x[np.asarray(rows)]
+    if bf16_weights:
+        xb = bf16_to_f32(x) if x.dtype == np.uint16 else bf16_to_f32(f32_to_bf16(np.asarray(x, f)))
+        wf = bf16_to_f32(w) if np.asarray(w).dtype == np.uint16 else np.asarray(w, f)
+    else:
+        xb, wf = np.asarray(x, f), np.asarray(w, f)
+    y = (xb.astype(np.float64) @ wf.astype(np.float64).T).astype(f)
+    if bf16_weights:
+        y = bf16_to_f32(f32_to_bf16(y))
+    if bias is not None:
+        y = (y + np.asarray(bias, f)[None, :]).astype(f)
+    return y
 
 
 # ---------------- LingBot full-row q/k RMSNorm + Wan RoPE ----------------

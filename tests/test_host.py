@@ -189,6 +189,19 @@ def test_device_entry_points_reject_bad_arguments(emb):
     assert L.emb_w8a16_gated_residual(buf, 1, 128, buf, buf, 4, 128, 128, None, None, 128, None, r, 128, o, 128, 0,
                                       C.c_void_p((1 << 20) + 256), None) == -1
     assert "workspace overlaps" in emb.last_error()
+    # dense weights: weight type, x type, K, ldw and a weight/out overlap are refused first
+    D = L.emb_dense_gated_residual
+    w = C.c_void_p(1 << 26)
+    args = lambda x32, K, wp, wt, ldw, out: (buf, x32, K, wp, wt, ldw, 4, K, 128, None, None, 128, None, r, 128, out,
+                                             128, 0, None, None)
+    assert D(*args(1, 128, w, emb.EMB_GGML_F16, 128, o)) == -4 and "weight_type" in emb.last_error()
+    assert D(*args(0, 128, w, emb.EMB_GGML_F32, 128, o)) == -4 and "f32 x" in emb.last_error()
+    assert D(*args(1, 120, w, emb.EMB_GGML_BF16, 120, o)) == -4 and "% 16" in emb.last_error()
+    assert D(*args(1, 130, w, emb.EMB_GGML_F32, 132, o)) == -4 and "% 4" in emb.last_error()
+    assert D(*args(1, 128, w, emb.EMB_GGML_BF16, 64, o)) == -1 and "ldw" in emb.last_error()
+    assert D(*args(1, 128, o, emb.EMB_GGML_BF16, 128, C.c_void_p((1 << 20) + 4096))) == -1
+    assert "overlaps the weights" in emb.last_error()
+    assert D(*args(1, 128, None, emb.EMB_GGML_BF16, 128, o)) == -1 and "null weight" in emb.last_error()
     assert L.emb_kv_gather(buf, buf, buf, 0, None, 16, buf, buf, 1, 128, None) == -1
     assert L.lingbot_runtime_kv_update_f32(buf, buf, buf, buf, buf, 4, 1, 64, 4, None) == -1
     assert "capacity" in emb.last_error()

@@ -724,3 +724,60 @@ def test_cpu_baseline_attention_matches_oracle(orc, threads):
                                     hkv2, d, 1 / 16, threads)
     want2 = orc.gqa_attention(q, k2, v2, n_q, n_k2, hq, hkv2, d, 1 / 16)
     assert np.allclose(got2, want2, rtol=0, atol=2e-5)
+
+
+# ---------------- dense-weight lin() (ggml CUDA mul_mat numerics) ----------------
+def test_dense_linear_known_answers(orc):
+    f = np.float32
+    # 257 ones: exact sum 257, which bf16 rounds to 256 (tie to even); f32 keeps it
+    x = np.ones((1, 257), f)
+    w = np.ones((1, 257), f)
+    assert orc.dense_linear(x, w, False)[0, 0] == 257.0
+    assert orc.dense_linear(x, orc.f32_to_bf16(w), True)[0, 0] == 256.0
+    # the bias is added after the bf16 rounding, as its own f32 node
+    b = np.array([0.5], f)
+    assert orc.dense_linear(x, w, False, bias=b)[0, 0] == 257.5
+    assert orc.dense_linear(x, orc.f32_to_bf16(w), True, bias=b)[0, 0] == 256.5
+    # x is rounded to bf16 first with bf16 weights (1 + 2^-9 -> 1), not with f32 ones
+    x1 = np.array([[1 + 2.0 ** -9]], f)
+    w1 = np.array([[1.0]], f)
+    assert orc.dense_linear(x1, w1, False)[0, 0] == f(1 + 2.0 ** -9)
+    assert orc.dense_linear(x1, orc.f32_to_bf16(w1), True)[0, 0] == 1.0
+    # and one rounding of the exact sum, not a rounding per partial sum:
+    # 2^24 + 1 + 1 is 2^24 + 2 exactly, which sequential f32 adds would lose
+    x3 = np.array([[2.0 ** 24, 1.0, 1.0]], f)
+    w3 = np.ones((1, 3), f)
+    assert orc.dense_linear(x3, w3, False)[0, 0] == f(2.0 ** 24 + 2)
+
+
+def test_dense_linear_index_order_brute_force(orc):
+    # w is [N][K] (ggml ne0 = K); a transposed operand or swapped index fails here
+    rng = np.random.default_rng(5)
+    M, K, N = 3, 5, 4
+    x = rng.integers(-8, 9, (M, K)).astype(np.float32)
+    w = rng.integers(-8, 9, (N, K)).astype(np.float32)
+    bias = rng.integers(-4, 5, N).astype(np.float32)
+    want = np.zeros((M, N), np.float32)
+    for m in range(M):
+        for n in range(N):
+            acc = 0.0
+            for k in range(K):
+                acc += float(x[m, k]) * float(w[n, k])
+            want[m, n] = acc + bias[n]
+    assert np.array_equal(orc.dense_linear(x, w, False, bias=bias), want)
+    assert np.array_equal(orc.dense_linear(x, orc.f32_to_bf16(w), True, bias=bias), want)  # small integers: exact
+    # bf16 x given as bits equals f32 x rounded by the oracle
+    xb = orc.f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    assert np.array_equal(orc.dense_linear(xb, orc.f32_to_bf16(w), True),
+                          orc.dense_linear(orc.bf16_to_f32(xb), orc.f32_to_bf16(w), True))
+    # rows= picks rows of x
+    assert np.array_equal(orc.dense_linear(x, w, False, rows=[2, 0]), orc.dense_linear(x, w, False)[[2, 0]])
+
+
+def test_gated_residual_without_residual(orc):
+    f = np.float32
+    y = np.array([[1.5, -0.0]], f)
+    g = np.array([[2.0, 3.0]], f)
+    out = orc.gated_residual(y, None, gate=g)
+    assert out[0, 0] == 3.0 and out[0, 1] == 0.0 and np.signbit(out[0, 1])  # -0 * 3 stays -0: no residual add
+    assert np.array_equal(orc.gated_residual(y, None), y)
