@@ -24,15 +24,19 @@
 // no synchronous copy.  restore (:8946-8952) and clear_pred (:8954-8965) are
 // elementwise kernels.
 //
-// One workgroup of 1024 threads; thread i owns the contiguous slot range
-// [i*R, (i+1)*R), R = ceil(capacity / 1024), so ascending-slot compaction is a
-// per-thread count, one exclusive scan (lane shuffles inside each wave, the 16
-// wave totals through LDS) and a per-thread write.  The eviction threshold
-// (the id below which every valid slot goes) is found by a bisection over the
-// id range of the valid slots, one counting pass a step.  For caches of up to
-// 14336 slots each thread's 14 slots stay in registers for the whole call
-// (staged through LDS with coalesced loads and written back the same way), so
-// the passes never wait on memory.
+// One workgroup of 512 threads (8 waves).  Wave w owns the contiguous slot
+// range [w*S, (w+1)*S), S a whole number of 64-slot rounds; in round r lane l
+// handles slot w*S + 64 r + l.  Every global access is then one coalesced
+// 64-slot row, and the ascending-slot ranks inside a wave are ballots and
+// mbcnt (lanes below in the same round, plus the earlier rounds' counts).
+// Across waves each step exchanges one row of per-wave values through LDS
+// with a single barrier, and every thread reads all 8 rows.  The eviction
+// threshold T (the id below which every valid slot goes) is the lowest valid
+// id when that id alone covers the eviction -- the steady state of a sliding
+// window, where the oldest chunk goes -- and otherwise a bisection over the id
+// range, one counting pass a step.  For caches of up to 16384 slots the
+// metadata of a lane's rounds stays in registers for the whole call (ids as
+// they are, the masks as one bit a round).
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -41,12 +45,10 @@
 
 namespace {
 
-constexpr int NT = 1024;
+constexpr int NT = 512;
 constexpr int NW = NT / 64;
-// Caches up to this many slots are staged in LDS (8-byte id + 1-byte mask a
-// slot, 126 KB at the config-3 capacity of 14040), larger ones are read in place.
-constexpr int LDS_SLOTS = 14336;
-static_assert(LDS_SLOTS % NT == 0, "whole staging rounds");
+constexpr int RMAX = 32;                     // rounds held in registers
+constexpr int REG_SLOTS = NW * 64 * RMAX;    // 16384
 
 struct DevCache {
     int64_t *id;
@@ -56,97 +58,57 @@ struct DevCache {
     int32_t legacy;
 };
 
-// Wave totals of the block reductions, in two buffers used alternately: a
-// reduction's single barrier then also orders it after the previous one's
-// reads of the other buffer.
-struct Scratch {
-    int64_t w64[2][NW][2];
-    int32_t w32[2][NW];
-    int flip;
+// One row of up to four per-wave values, in two buffers used alternately: an
+// exchange's single barrier then also orders it after every thread's reads of
+// the other buffer in the exchange before.
+struct Rows {
+    int64_t v[2][NW][4];
 };
 
-// Exclusive prefix of v over the workgroup (threads in order) and the total:
-// an inclusive scan inside each wave by lane shuffles, then the 16 wave totals
-// through LDS.  One barrier.
-__device__ __forceinline__ int32_t block_scan(int32_t v, Scratch &sc, int &flip, int32_t *total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int32_t x = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int32_t y = __shfl_up(x, off, 64);
-        if (lane >= off) x += y;
-    }
-    int32_t *buf = sc.w32[flip];
-    flip ^= 1;
-    if (lane == 63) buf[w] = x;
-    __syncthreads();
-    int32_t before = 0, all = 0;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) {
-        const int32_t a = buf[i];
-        before += i < w ? a : 0;
-        all += a;
-    }
-    *total = all;
-    return before + x - v;
+__device__ __forceinline__ int32_t lanes_below(uint64_t m) {
+    return (int32_t)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-__device__ __forceinline__ int32_t block_sum(int32_t v, Scratch &sc, int &flip) {
-    int32_t total;
-    block_scan(v, sc, flip, &total);
-    return total;
+// A 64-bit DPP lane move (both halves with the same pattern; every pattern
+// used here reads a lane of the same row, so all lanes are written).
+template <int CTRL>
+__device__ __forceinline__ int64_t dpp64(int64_t v) {
+    const uint64_t u = (uint64_t)v;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// (max a, max b) over the workgroup.  One barrier.
-__device__ __forceinline__ void block_max2(int64_t &a, int64_t &b, Scratch &sc, int &flip) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const int64_t ya = __shfl_xor(a, off, 64), yb = __shfl_xor(b, off, 64);
-        a = ya > a ? ya : a;
-        b = yb > b ? yb : b;
-    }
-    int64_t(*buf)[2] = sc.w64[flip];
-    flip ^= 1;
-    if (lane == 0) {
-        buf[w][0] = a;
-        buf[w][1] = b;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < NW; ++i) {
-        a = buf[i][0] > a ? buf[i][0] : a;
-        b = buf[i][1] > b ? buf[i][1] : b;
-    }
+__device__ __forceinline__ int64_t lane64(int64_t v, int l) {
+    const uint64_t u = (uint64_t)v;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// The slots a thread owns, [s0, s0 + n), and their (mask, id).  REG: at
-// most PER slots, held in registers for the whole call (staged through LDS
-// with coalesced loads; the slots a call changes are stored back), so every
-// pass below is register arithmetic.  Otherwise the passes read and write global memory in
-// place (caches past LDS_SLOTS).
-constexpr int PER = LDS_SLOTS / NT;
+// Wave sum of v, uniform (the same lane pattern as wave_ext below).
+__device__ __forceinline__ int32_t wave_sum(int32_t v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xf, 0xf, false);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+           __builtin_amdgcn_readlane(v, 48);
+}
 
-template <bool REG>
-struct Own {
-    int32_t s0, n;
-    uint8_t *gm;
-    int64_t *gi;
-    uint8_t rm[REG ? PER : 1];
-    int64_t ri[REG ? PER : 1];
-
-    // f(i, s, mask&, id&) for each owned slot in ascending order
-    template <typename F>
-    __device__ __forceinline__ void each(F &&f) {
-        if constexpr (REG) {
-#pragma unroll
-            for (int i = 0; i < PER; ++i)
-                if (i < n) f(i, s0 + i, rm[i], ri[i]);
-        } else {
-            for (int32_t i = 0; i < n; ++i) f(i, s0 + i, gm[s0 + i], gi[s0 + i]);
-        }
-    }
-};
+// Wave minimum (MAX = false) or maximum of v, uniform: within quads (lane
+// xor 1, xor 2), then across the two quads of each 8-lane half (half mirror)
+// and the two halves of each 16-lane row (row mirror), then the four rows.
+// All 64 lanes must be active.
+template <bool MAX>
+__device__ __forceinline__ int64_t wave_ext(int64_t v) {
+    auto pick = [](int64_t a, int64_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    v = pick(v, dpp64<0xB1>(v));   // quad_perm(1, 0, 3, 2)
+    v = pick(v, dpp64<0x4E>(v));   // quad_perm(2, 3, 0, 1)
+    v = pick(v, dpp64<0x141>(v));  // row_half_mirror
+    v = pick(v, dpp64<0x140>(v));  // row_mirror
+    return pick(pick(lane64(v, 0), lane64(v, 16)), pick(lane64(v, 32), lane64(v, 48)));
+}
 
 // status: 0 = done, EMB_ERR_CAPACITY = too few slots even after evicting every
 // valid slot (the evictions persist, as in the reference).
@@ -155,138 +117,252 @@ __global__ __launch_bounds__(NT) void meta_update_kernel(DevCache c, int32_t key
                                                          int32_t *__restrict__ slots, int32_t *__restrict__ valid,
                                                          int32_t *__restrict__ n_valid,
                                                          int32_t *__restrict__ status) {
-    __shared__ Scratch sc;
+    __shared__ Rows rows;
     int flip = 0;
-    __shared__ int64_t lid[REG ? LDS_SLOTS : 1];
-    __shared__ uint8_t lmask[REG ? LDS_SLOTS : 1];
-    const int t = threadIdx.x;
-    const int32_t R = (c.capacity + NT - 1) / NT;
-    Own<REG> own;
-    own.s0 = min(t * R, c.capacity);
-    own.n = min(own.s0 + R, c.capacity) - own.s0;
-    own.gm = c.mask;
-    own.gi = c.id;
-    uint32_t dirty = 0;  // REG: owned slots this call changed (bit i = slot s0 + i)
-    if constexpr (REG) {  // coalesced loads into LDS, then each thread's range into registers
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            const int32_t s = t + j * NT;
-            if (s < c.capacity) {
-                lid[s] = c.id[s];
-                lmask[s] = c.mask[s];
-            }
+    const int t = threadIdx.x, lane = t & 63;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int32_t cap = c.capacity;
+    const int32_t S = ((cap + NW - 1) / NW + 63) / 64 * 64;  // slots a wave owns, whole rounds
+    const int32_t nr = S / 64;
+    const int32_t w0 = w * S, wend = min(w0 + S, cap);
+
+    // exchange up to four per-wave values; returns the buffer every thread then reads
+    auto exchange = [&](int64_t a, int64_t b, int64_t d, int64_t e) __attribute__((always_inline)) {
+        int64_t(*buf)[4] = rows.v[flip];
+        flip ^= 1;
+        if (lane == 0) {
+            buf[w][0] = a;
+            buf[w][1] = b;
+            buf[w][2] = d;
+            buf[w][3] = e;
         }
         __syncthreads();
+        return buf;
+    };
+
+    // f(r, s, present, mask&, id&) for each round in ascending slot order; the
+    // whole wave calls f every round (absent lanes with present = false), so f
+    // may take ballots.  Not REG: changes of mask / id are stored in place.
+    int64_t ri[REG ? RMAX : 1];
+    uint32_t mbits = 0;  // REG: bit r = mask of round r's slot (nonzero -> 1)
+    uint32_t dirty = 0;  // REG: rounds whose slot this lane changed
+    auto each = [&](auto &&f) __attribute__((always_inline)) {
+        if constexpr (REG) {
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            own.rm[i] = i < own.n ? lmask[own.s0 + i] : 0;
-            own.ri[i] = i < own.n ? lid[own.s0 + i] : 0;
+            for (int r = 0; r < RMAX; ++r) {
+                if (r < nr) {
+                    const int32_t s = w0 + r * 64 + lane;
+                    uint8_t m = (mbits >> r) & 1u;
+                    f(r, s, s < wend, m, ri[r]);
+                    mbits = (mbits & ~(1u << r)) | ((uint32_t)(m != 0) << r);
+                }
+            }
+        } else {
+            for (int32_t r = 0; r < nr; ++r) {
+                const int32_t s = w0 + r * 64 + lane;
+                const bool in = s < wend;
+                uint8_t m = in ? c.mask[s] : 0;
+                int64_t id = in ? c.id[s] : -1;
+                const uint8_t m0 = m;
+                const int64_t id0 = id;
+                f(r, s, in, m, id);
+                if (in && (m != m0 || id != id0)) {
+                    c.mask[s] = m;
+                    c.id[s] = id;
+                }
+            }
+        }
+    };
+    if constexpr (REG) {
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+            const int32_t s = w0 + r * 64 + lane;
+            const bool in = r < nr && s < wend;
+            if (in && c.mask[s]) mbits |= 1u << r;
+            ri[r] = in ? c.id[s] : -1;
         }
     }
 
-    // free count and the id range of the valid slots
-    int32_t nfree = 0;
-    int64_t idmin = LLONG_MAX, idmax = LLONG_MIN;
-    own.each([&](int, int32_t, uint8_t &m, int64_t &id) {
-        if (!m) {
-            ++nfree;
-        } else {
-            idmin = id < idmin ? id : idmin;
-            idmax = id > idmax ? id : idmax;
+    // One pass: free count, the id range of the valid slots and how many hold
+    // the lowest id (counts kept per lane and summed once: no per-round
+    // ballot chain).  A wave's slots in range: its share of [0, cap).
+    auto in_range = [&](int i) { return max(0, min(S, cap - i * S)); };
+    int32_t nfree = 0, cmn = 0;
+    int64_t mn = LLONG_MAX, mx = LLONG_MIN;
+    each([&](int, int32_t, bool in, uint8_t &m, int64_t &id) {
+        nfree += in && !m;
+        if (in && m) {
+            cmn = id < mn ? 1 : cmn + (id == mn);
+            mn = id < mn ? id : mn;
+            mx = id > mx ? id : mx;
         }
     });
-    int32_t free_total = block_sum(nfree, sc, flip);
-    const int32_t used_total = c.capacity - free_total;
-    bool ok = true;
+    nfree = wave_sum(nfree);
+    {
+        const int64_t wmn = wave_ext<false>(mn);
+        cmn = wave_sum(mn == wmn ? cmn : 0);
+        mn = wmn;
+    }
+    mx = wave_ext<true>(mx);
+    int32_t free_total = 0, atmin_total = 0, atmin_before = 0;
+    int32_t frank = 0, vrank = 0, nv_total = 0;  // final ranks: this wave's first free / listed rank
+    int64_t idmin = LLONG_MAX, idmax = LLONG_MIN;
+    // per-wave (free, valid) after the call's evictions -> ranks
+    auto ranks = [&](auto &&nf_of, auto &&nv_of) __attribute__((always_inline)) {
+        int32_t fbefore = 0;
+        nv_total = 0;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            const int32_t nfi = nf_of(i), nvi = nv_of(i);
+            const int32_t chosen = min(max(key_size - fbefore, 0), nfi);
+            if (i == w) {
+                frank = fbefore;
+                vrank = nv_total;
+            }
+            fbefore += nfi;
+            nv_total += nvi + chosen;
+        }
+    };
+    int32_t nfree_of[NW];  // per wave; kept here, the exchange buffer is reused
+    {
+        int64_t(*b)[4] = exchange(nfree, mn, cmn, mx);
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            nfree_of[i] = (int32_t)b[i][0];
+            free_total += nfree_of[i];
+            idmin = b[i][1] < idmin ? b[i][1] : idmin;
+            idmax = b[i][3] > idmax ? b[i][3] : idmax;
+        }
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            const int32_t c_i = b[i][1] == idmin ? (int32_t)b[i][2] : 0;
+            atmin_total += c_i;
+            atmin_before += i < w ? c_i : 0;
+        }
+    }
+    const int32_t used_total = cap - free_total;
+    int32_t used_after = used_total;
 
     if (free_total < key_size && used_total > 0) {
-        // evict the e lowest (id, slot) valid slots
+        // evict the e lowest (id, slot) valid slots: every valid slot with
+        // id < T and the first take_at (ascending slot) with id == T
         const int32_t e = min(key_size - free_total, used_total);
-        int64_t lo = -idmin, hi = idmax;
-        block_max2(lo, hi, sc, flip);
-        lo = -lo;
-        // smallest T with count(valid, id <= T) >= e
-        while (lo < hi) {
-            const int64_t mid = lo + ((hi - lo) >> 1);
-            int32_t n = 0;
-            own.each([&](int, int32_t, uint8_t &m, int64_t &id) { n += m && id <= mid; });
-            if (block_sum(n, sc, flip) >= e)
-                hi = mid;
-            else
-                lo = mid + 1;
+        int64_t T = idmin;
+        int32_t below_total = 0, at_total = atmin_total, at_before = atmin_before;
+        if (at_total < e) {
+            // smallest T in (idmin, idmax] with count(valid, id <= T) >= e
+            int64_t lo = idmin + 1, hi = idmax;
+            while (lo < hi) {
+                const int64_t mid = lo + ((hi - lo) >> 1);
+                int32_t n = 0;
+                each([&](int, int32_t, bool in, uint8_t &m, int64_t &id) { n += in && m && id <= mid; });
+                int64_t(*b)[4] = exchange(wave_sum(n), 0, 0, 0);
+                int32_t tot = 0;
+#pragma unroll
+                for (int i = 0; i < NW; ++i) tot += (int32_t)b[i][0];
+                if (tot >= e)
+                    hi = mid;
+                else
+                    lo = mid + 1;
+            }
+            T = lo;
+            int32_t below = 0, at = 0;
+            each([&](int, int32_t, bool in, uint8_t &m, int64_t &id) {
+                below += in && m && id < T;
+                at += in && m && id == T;
+            });
+            int64_t(*b)[4] = exchange(wave_sum(below), wave_sum(at), 0, 0);
+            at_total = at_before = 0;
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                below_total += (int32_t)b[i][0];
+                at_before += i < w ? (int32_t)b[i][1] : 0;
+                at_total += (int32_t)b[i][1];
+            }
         }
-        const int64_t T = lo;
-        int32_t below = 0, at = 0;
-        own.each([&](int, int32_t, uint8_t &m, int64_t &id) {
-            if (m) {
-                below += id < T;
-                at += id == T;
-            }
-        });
-        const int32_t below_total = block_sum(below, sc, flip);
-        int32_t at_total;
-        int32_t rank = block_scan(at, sc, flip, &at_total);  // ascending slot order among id == T
         const int32_t take_at = e - below_total;
-        own.each([&](int i, int32_t s, uint8_t &m, int64_t &id) {
-            if (!m) return;
-            bool ev = id < T;
-            if (id == T) ev = rank++ < take_at;
-            if (ev) {
-                m = 0;
-                id = -1;
-                dirty |= 1u << i;
-                if (c.legacy) c.is_pred[s] = 0;
-            }
-        });
+        int32_t nev = 0;
+        auto evict = [&](int r, int32_t s, uint8_t &m, int64_t &id) __attribute__((always_inline)) {
+            m = 0;
+            id = -1;
+            dirty |= 1u << r;
+            ++nev;
+            if (c.legacy) c.is_pred[s] = 0;
+        };
+        if (take_at >= at_total) {  // the whole id == T group goes (a window's oldest chunk): no ranks
+            each([&](int r, int32_t s, bool in, uint8_t &m, int64_t &id) {
+                if (in && m && id <= T) evict(r, s, m, id);
+            });
+        } else {
+            int32_t run = at_before;
+            each([&](int r, int32_t s, bool in, uint8_t &m, int64_t &id) {
+                const bool valid_slot = in && m;
+                const uint64_t bm = __ballot(valid_slot && id == T);
+                const int32_t rank = run + lanes_below(bm);
+                run += (int32_t)__popcll(bm);
+                if (valid_slot && (id < T || (id == T && rank < take_at))) evict(r, s, m, id);
+            });
+        }
+        nev = wave_sum(nev);
         free_total += e;
+        used_after = used_total - e;
+        if (free_total >= key_size) {
+            int64_t(*b)[4] = exchange(nev, 0, 0, 0);
+            ranks([&](int i) { return nfree_of[i] + (int32_t)b[i][0]; },
+                  [&](int i) { return in_range(i) - (nfree_of[i] + (int32_t)b[i][0]); });
+        }
+    } else if (free_total >= key_size) {
+        ranks([&](int i) { return nfree_of[i]; }, [&](int i) { return in_range(i) - nfree_of[i]; });
     }
-    if (free_total < key_size) {
-        ok = false;
-    } else {
-        // new_id = next_id() after the evictions, before the stamps; the first
-        // key_size free slots in ascending order
-        int32_t nf = 0;
-        int64_t mx = -1;
-        own.each([&](int, int32_t, uint8_t &m, int64_t &id) {
-            if (!m)
-                ++nf;
-            else
-                mx = id > mx ? id : mx;
-        });
-        int64_t unused64 = 0;
-        block_max2(mx, unused64, sc, flip);
-        const int64_t new_id = mx + 1;
-        int32_t unused;
-        int32_t frank = block_scan(nf, sc, flip, &unused);  // free rank of this range's first free slot
-        // slots listed after the call: the visible ones and the chosen ones
-        // (which modes 1/2 make visible and mode 0 lists as temporaries); the
-        // chosen ones of this range are its free slots of rank below key_size
-        const int32_t nchosen = min(max(key_size - frank, 0), nf);
-        int32_t nv_total;
-        int32_t vrank = block_scan(own.n - nf + nchosen, sc, flip, &nv_total);
-        own.each([&](int i, int32_t s, uint8_t &m, int64_t &id) {
-            bool listed = m != 0;
-            if (!listed) {
-                if (frank < key_size) {
-                    slots[frank] = s;
-                    dirty |= 1u << i;
-                    id = new_id;
-                    c.is_pred[s] = mode == 1;
-                    if (mode != 0) m = 1;
-                    listed = true;
-                }
-                ++frank;
+    const bool ok = free_total >= key_size;
+    if (ok) {
+        // new_id = next_id() after the evictions, before the stamps.  Evictions
+        // take the lowest ids first, so a valid slot that remains leaves idmax
+        // the largest id; none remaining leaves next_id() = 0.
+        const int64_t new_id = used_after > 0 ? idmax + 1 : 0;
+        // chosen: the first key_size free slots in ascending order; listed
+        // after the call: the visible ones and the chosen ones (which modes 1/2
+        // make visible and mode 0 lists as temporaries).  When every slot ends
+        // up listed (a full window) the list is 0 .. cap-1 and needs no ranks.
+        const bool all_listed = nv_total == cap;
+        auto stamp = [&](int r, int32_t s, bool in, uint8_t &m, int64_t &id) __attribute__((always_inline)) {
+            const bool fre = in && !m;
+            const uint64_t fm = __ballot(fre);
+            const int32_t fr = frank + lanes_below(fm);
+            frank += (int32_t)__popcll(fm);
+            const bool chosen = fre && fr < key_size;
+            const bool listed = (in && m) || chosen;
+            if (chosen) {
+                slots[fr] = s;
+                id = new_id;
+                c.is_pred[s] = mode == 1;
+                if (mode != 0) m = 1;
+                dirty |= 1u << r;
             }
-            if (valid && listed) valid[vrank++] = s;
-        });
+            return listed;
+        };
+        if (all_listed || !valid) {
+            each([&](int r, int32_t s, bool in, uint8_t &m, int64_t &id) {
+                stamp(r, s, in, m, id);
+                if (valid && in) valid[s] = s;
+            });
+        } else {
+            each([&](int r, int32_t s, bool in, uint8_t &m, int64_t &id) {
+                const bool listed = stamp(r, s, in, m, id);
+                const uint64_t lm = __ballot(listed);
+                if (listed) valid[vrank + lanes_below(lm)] = s;
+                vrank += (int32_t)__popcll(lm);
+            });
+        }
         if (t == 0 && n_valid) n_valid[0] = nv_total;
     }
     if constexpr (REG) {  // write back the changed slots (evictions persist on failure too)
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            if ((dirty >> i) & 1u) {
-                c.id[own.s0 + i] = own.ri[i];
-                c.mask[own.s0 + i] = own.rm[i];
+        for (int r = 0; r < RMAX; ++r) {
+            if ((dirty >> r) & 1u) {
+                const int32_t s = w0 + r * 64 + lane;
+                c.id[s] = ri[r];
+                c.mask[s] = (uint8_t)((mbits >> r) & 1u);
             }
         }
     }
@@ -365,7 +441,7 @@ int emb_dev_cache_update(const emb_dev_slot_cache *c, int32_t key_size, int32_t 
     EMB_CHECK_ARG(key_size > 0, "key_size must be positive");
     EMB_CHECK_ARG(mode >= 0 && mode <= 2, "mode must be 0, 1 or 2");
     EMB_CHECK_ARG(slots && status, "null slots / status");
-    if (c->capacity <= LDS_SLOTS)
+    if (c->capacity <= REG_SLOTS)
         hipLaunchKernelGGL(meta_update_kernel<true>, dim3(1), dim3(NT), 0, stream, dev(c), key_size, mode, slots, valid,
                            n_valid, status);
     else
