@@ -967,7 +967,7 @@ def main():
     ap.add_argument("--configs", default="cfg1,cfg2,cfg3,cfg4,cfg5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="profiling targets: cfg1_attn (the headline kernel loop), cfg2_attn, cfg3_attn, cfg4_attn, cfg5_gemm, "
+                    help="profiling targets: cfg1_attn (the headline kernel loop), cfg2_attn, cfg3_attn, cfg3_meta, cfg4_attn, cfg5_gemm, "
                          "copy_calib (a plain 256 MiB device copy, the PMC byte-counter calibration)")
     ap.add_argument("--traffic-summary", default="", metavar="DIR",
                     help="write profiles/" + TRAFFIC_FILE + " from the four rocprofv3 --pmc runs under DIR "
@@ -1019,6 +1019,10 @@ def main():
         return
     if args.only == "cfg5_gemm":
         bench_cfg5(c, args.steps, args.warmup)
+        log("profile loop done")
+        return
+    if args.only == "cfg3_meta":  # device slot metadata, 30 layer caches at the config-3 shape
+        log("cfg3_meta " + json.dumps(bench_meta(c, args.steps)))
         log("profile loop done")
         return
     if args.only == "cfg3_attn":
