@@ -143,8 +143,9 @@ class PagedLayers:
         self.ws = None
         torch.cuda.synchronize()
 
-    def set_splits(self, splits):
+    def set_splits(self, splits, split_keys=0):
         self.splits = splits
+        self.split_keys = split_keys
         if splits > 1:
             nb = self.c.emb.attn_workspace_bytes(self.L, self.n_new, self.hq, self.hkv, self.d, splits)
             self.ws = self.c.torch.zeros(nb // 4 + 64, dtype=self.c.torch.float32, device=self.c.dev)
@@ -165,7 +166,7 @@ class PagedLayers:
                                    n_keys=None if self.uniform else self.nk,
                                    n_keys_uniform=self.n_keys[0] if self.uniform else 0,
                                    block_tables=self.bt, bt_stride=self.bt_stride, splits=self.splits,
-                                   workspace=self.ws, stream=stream)
+                                   workspace=self.ws, stream=stream, split_keys=getattr(self, "split_keys", 0))
 
     # algorithmic bytes of one attention launch: K/V of every key once, Q, O (f32), tables
     def attn_bytes(self):
@@ -347,22 +348,27 @@ def bench_cfg4(c: Ctx, steps, warmup):
     lens_all = [300 + g.next() % 901 for _ in range(64)]
     for B in (1, 8, 32, 64):
         P = PagedLayers(c, 0xE3BD0004 + B, lens_all[:B], 51, 8, 1, 256, n_steps=2)
+        # (splits, split_keys): uniform splits, and per-session splits sized
+        # by each session's key count (split_keys > 0)
         best = None
-        for sp in (1, 2, 4, 8):
-            if B >= 32 and sp > 2:
+        sweep = {}
+        for sp, sk in ((1, 0), (2, 0), (4, 0), (8, 0), (3, 384), (4, 256), (4, 320), (6, 192), (8, 128)):
+            if B >= 32 and sk == 0 and sp > 2:
                 continue
-            P.set_splits(sp)
+            P.set_splits(sp, sk)
             ms, _ = c.time_graph(lambda st: P.attend(0, st, 1 / 16), steps, warmup)
+            sweep[f"{sp}/{sk}"] = ms * 1e3
             if best is None or ms < best[1]:
-                best = (sp, ms)
-        P.set_splits(best[0])
+                best = ((sp, sk), ms)
+        P.set_splits(*best[0])
 
         def one(st):
             P.append(0, st)
             P.attend(0, st, 1 / 16)
         ms_all, _ = c.time_graph(one, steps, warmup)
         ab = P.attn_bytes()
-        res[f"B{B}"] = dict(attn_us=best[1] * 1e3, append_plus_attn_us=ms_all * 1e3, splits=best[0],
+        res[f"B{B}"] = dict(attn_us=best[1] * 1e3, append_plus_attn_us=ms_all * 1e3, splits=best[0][0],
+                            split_keys=best[0][1], split_sweep_us=sweep,
                             attn_gbs=ab / (best[1] * 1e-3) / 1e9,
                             attn_hbm_frac=ab / (best[1] * 1e-3) / 1e9 / PEAK_HBM_GBS,
                             survey_bytes=P.survey_step_bytes(),

@@ -142,6 +142,7 @@ struct KParams {
     int32_t max_q;
     int32_t row_tiles;
     int32_t splits;
+    int32_t split_keys;  // > 0: a sequence of n keys takes min(splits, ceil(n / split_keys)) splits
     int32_t total_wg;
     float scale;
     float c_log2;     // scale * log2(e)
@@ -209,6 +210,12 @@ __device__ __forceinline__ int32_t page_of(const int32_t *bt_b, int32_t slot) {
 }
 
 // Element offsets inside a stage (see the header comment).
+// Splits a sequence with nk keys takes (the merge kernel reads the same count).
+__device__ __forceinline__ int32_t seq_splits(const KParams &p, int32_t nk) {
+    if (p.split_keys <= 0) return p.splits;
+    return min(p.splits, max(1, (nk + p.split_keys - 1) / p.split_keys));
+}
+
 template <int D>
 __device__ __forceinline__ int k_off(int row, int chunk) {
     return row * D + ((chunk ^ (row & Geo<D>::SWZ)) << 3);
@@ -661,8 +668,10 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
     }
     int32_t t_lo = k_lo / G::KT, t_hi = (max(k_hi, k_lo) + G::KT - 1) / G::KT;
     if (p.splits > 1) {
+        const int32_t ns = seq_splits(p, nk);
+        if (split >= ns) return;  // a short sequence of a ragged batch: fewer splits (uniform per workgroup)
         const int32_t nt = t_hi - t_lo;
-        const int32_t per = (nt + p.splits - 1) / p.splits;
+        const int32_t per = (nt + ns - 1) / ns;
         const int32_t a = t_lo + split * per;
         t_hi = min(t_hi, a + per);
         t_lo = min(a, t_hi);
@@ -1259,6 +1268,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
         if (row >= nq * p.G) continue;
         const int64_t rows_per_unit = (int64_t)blocks_per_unit * 32;
         const int64_t unit0 = (int64_t)(b * p.hkv + kvh) * p.splits;
+        const int32_t ns = seq_splits(p, p.n_keys ? p.n_keys[b] : p.nk_single);
         float ms[MS], ls[MS];
         int ks[MS];
         u32x2 os[MS][NCH];
@@ -1269,7 +1279,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
             ks[s] = 0;
 #pragma unroll
             for (int j = 0; j < NCH; ++j) os[s][j] = u32x2{0u, 0u};
-            if (s < p.splits) {
+            if (s < ns) {
                 const int64_t u = (unit0 + s) * rows_per_unit;
                 const f32x4 ml = *reinterpret_cast<const f32x4 *>(p.ws_ml + (u + row) * 4);
                 ms[s] = ml[0];
@@ -1620,6 +1630,8 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     kp.G = a->hq / a->hkv;
     kp.row_tiles = (int32_t)(((int64_t)a->max_q * kp.G + ROWS_PER_WG - 1) / ROWS_PER_WG);
     kp.splits = splits;
+    EMB_CHECK_ARG(a->split_keys >= 0, "split_keys must be >= 0");
+    kp.split_keys = splits > 1 ? a->split_keys : 0;
     const int64_t total = (int64_t)a->batch * a->hkv * splits * kp.row_tiles;
     EMB_CHECK_ARG(total < INT_MAX / 2, "grid too large");
     kp.total_wg = (int32_t)total;

@@ -45,6 +45,7 @@ class AttnArgs(C.Structure):
         ("n_keys_uniform", C.c_int32),
         ("out_bf16_round", C.c_int32),
         ("p_bf16", C.c_int32),
+        ("split_keys", C.c_int32),
     ]
 
 
@@ -576,7 +577,8 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
                     valid_stride=0, mask_kind=EMB_MASK_FULL, chunk=0, window=-1, mask=None,
                     mask_q_stride=0, mask_batch_stride=0, block_map=None, block_size=0,
                     block_map_cols=0, block_map_batch_stride=0, splits=1, workspace=None,
-                    n_keys_uniform=0, out_bf16_round=False, stream=None, noalloc=False, p_bf16=False):
+                    n_keys_uniform=0, out_bf16_round=False, stream=None, noalloc=False, p_bf16=False,
+                    split_keys=0):
     a = AttnArgs()
     a.q = ptr(q); a.q_is_f32 = int(q_is_f32)
     a.q_stride = q_stride if q_stride is not None else hq * d
@@ -594,6 +596,7 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
     a.splits = splits; a.workspace = ptr(workspace); a.n_keys_uniform = n_keys_uniform
     a.out_bf16_round = int(out_bf16_round)
     a.p_bf16 = int(p_bf16)
+    a.split_keys = int(split_keys)
     if noalloc:  # split-K partials in the library's scratch (workspace must be None)
         return check(lib().emb_paged_attention_noalloc(C.byref(a), stream_ptr(stream)), "emb_paged_attention_noalloc")
     return check(lib().emb_paged_attention(C.byref(a), stream_ptr(stream)), "emb_paged_attention")

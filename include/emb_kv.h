@@ -411,6 +411,11 @@ typedef struct emb_attn_args {
                                           models/smolvla.cpp:264-266, :317-318); a two-pass
                                           kernel, unsplit (splits 0 or 1), masks FULL, CHUNK,
                                           TOKEN or ADD; the f16 V shadow is not read */
+    int32_t split_keys;                /* with splits > 1: 0 = every sequence takes `splits`
+                                          splits; > 0 = a sequence of n keys takes
+                                          min(splits, ceil(n / split_keys)) (at least 1), so
+                                          short sequences of a ragged batch are not cut into
+                                          splits that cost more than they save */
 } emb_attn_args;
 
 size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_t hkv,

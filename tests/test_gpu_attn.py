@@ -205,19 +205,22 @@ def test_null_block_tables_are_identity(emb, orc, torch_dev, d, hq, hkv, mask):
         assert_close(outs[(1, "null")][b * nq:(b + 1) * nq], ref, f"null tables seq {b}")
 
 
-@pytest.mark.parametrize("B,splits", [(1, 8), (8, 8), (32, 2), (64, 1), (64, 2)])
-def test_multi_session_sweep(emb, orc, torch_dev, B, splits):
+@pytest.mark.parametrize("B,splits,split_keys", [(1, 8, 0), (8, 8, 0), (32, 2, 0), (64, 1, 0), (64, 2, 0),
+                                                   (8, 8, 128), (32, 4, 384), (64, 4, 320), (64, 3, 512)])
+def test_multi_session_sweep(emb, orc, torch_dev, B, splits, split_keys):
     """cfg4 at every batch the bench times, with its prefix lengths and split
     choices: session b's prefix is 300 + x_b % 901, x_b the b-th output of
     std::mt19937_64(0xE3BD0004); 51 queries x 8 heads over prefix + 51 keys,
     pages scattered in one pool.  All rows of every session at B <= 8; 24
-    sampled rows of every session at B = 32 and 64."""
+    sampled rows of every session at B = 32 and 64.  split_keys > 0: each
+    session takes min(splits, ceil(keys / split_keys)) splits, so sessions of
+    one batch are cut differently and the merge reads a count per session."""
     torch, dev = torch_dev
     lens = [300 + orc.lib().orc_mt64_nth(0xE3BD0004, b + 1) % 901 for b in range(B)]
     assert 300 <= min(lens) and max(lens) <= 1200
     rng = np.random.default_rng(0xE3BD0004 + B)
     s = Seqs(orc, rng, [int(x) + 51 for x in lens], [51] * B, 8, 1, 256)
-    got = s.run(emb, torch, dev, 1 / 16, splits=splits)
+    got = s.run(emb, torch, dev, 1 / 16, splits=splits, split_keys=split_keys)
     for b in range(B):
         rows = None if B <= 8 else np.sort(rng.choice(51, 3, replace=False))
         ref = s.oracle(orc, b, 1 / 16, rows=rows)
@@ -225,6 +228,20 @@ def test_multi_session_sweep(emb, orc, torch_dev, B, splits):
             assert_close(got[b], ref, f"B={B} session {b}")
         else:
             assert_close(got[b][rows], ref[rows], f"B={B} session {b} rows {rows.tolist()}")
+
+
+def test_split_keys_uniform_batch(emb, orc, torch_dev):
+    """split_keys on the bounds-free form (every sequence n_keys_uniform keys):
+    867 keys with splits 8 and split_keys 300 run 3 splits; the result equals
+    the same call with splits 3 bit for bit, and the oracle within the bar."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xE3BD0000 + 7)
+    s = Seqs(orc, rng, [867, 867], [51, 51], 8, 1, 256)
+    a = s.run(emb, torch, dev, 1 / 16, splits=8, uniform=True, split_keys=300)
+    b = s.run(emb, torch, dev, 1 / 16, splits=3, uniform=True)
+    for i in range(2):
+        assert np.array_equal(a[i], b[i]), f"sequence {i}: split_keys 300 of 8 differs from 3 splits"
+        assert_close(a[i], s.oracle(orc, i, 1 / 16), f"sequence {i}")
 
 
 def test_prefill_prefix_lm_rows(emb, orc, torch_dev):

@@ -208,6 +208,10 @@ def test_device_entry_points_reject_bad_arguments(emb):
     with pytest.raises(RuntimeError, match="head_dim"):
         emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=1, hq=8, hkv=1, d=96,
                             max_q=4, scale=0.1, capacity=64)
+    with pytest.raises(RuntimeError, match="split_keys"):
+        emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=1, hq=8, hkv=1, d=256,
+                            max_q=4, scale=0.1, capacity=64, n_keys_uniform=64, splits=2, workspace=256,
+                            split_keys=-1)
     with pytest.raises(RuntimeError, match="head counts"):
         emb.paged_attention(q=256, out=256, k_pool=256, v_pool=256, batch=1, hq=6, hkv=4, d=128,
                             max_q=4, scale=0.1, capacity=64)
