@@ -593,9 +593,6 @@ __global__ __launch_bounds__(256, 2) void f32_gemm_kernel(GParams p) {
 // the same k of column n.  x rows are 128 bytes; the 16-byte chunk c of row r
 // sits at granule c ^ ((r >> 1) & 7) of the row, so the 16 rows a quarter-wave
 // reads hit 16 different bank groups (W: half h at slot h ^ ((n >> 3) & 1)).
-constexpr int TBN = 256;                        // tile columns
-constexpr int TX = 256 * BK;                    // bf16 elements of one x image
-constexpr int TW = (BK / 16) * TBN * 16;        // bf16 elements of one W image
 constexpr uint32_t RSRC_W3 = 0x00020000u;       // raw buffer, 32-bit elements
 
 __device__ __forceinline__ u32x4 buf_desc(const void *base, uint32_t bytes) {
@@ -631,8 +628,9 @@ __device__ __forceinline__ void lds_copy16(const u32x4 &d, uint32_t m0, uint32_t
 #pragma clang diagnostic pop
 
 
-// One thread's W words of a k-tile: thread t takes band t / 128 of the tile,
-// 64-column group (t / 32) % 4, and in it the words j = 2h, 2h + 1 (h = q / 2)
+// One thread's W words of a k-tile (NG 64-column groups in the tile): thread t
+// takes band t / (32 NG) of the tile, 64-column group (t / 32) % NG, and in it
+// the words j = 2h, 2h + 1 (h = q / 2)
 // of the 4 columns with n % 8 = (t % 32) / 4 and (n / 8) % 8 = (q % 2) * 4 + e,
 // q = t % 4 (the layout recap at the top).  Loaded by inline asm, so the
 // kernel counts them with its copies (the compiler would wait for them with
@@ -641,11 +639,13 @@ struct WRegs {
     u32x4 w0, w1;
 };
 
+template <int NG>
 __device__ __forceinline__ void load_w(WRegs &r, const GParams &p, int32_t n0, int32_t k0, int tid) {
-    const int band = tid >> 7, grp = (tid >> 5) & 3, idx = tid & 31;
+    const int band = tid / (32 * NG), grp = (tid >> 5) % NG, idx = tid & 31;
     const int n8 = idx >> 2, q = idx & 3;
     const int c0 = n8 * 32 + (q & 1) * 4 + (q >> 1) * 16;
-    const int32_t kb = (k0 >> 4) + band;
+    // bands past K (the loads issued beyond the last k-tile) read the last band
+    const int32_t kb = min((k0 >> 4) + band, (p.K >> 4) - 1);
     // a group past N reads the last one instead (its columns are never stored)
     const int32_t col64 = min((n0 >> 6) + grp, p.N / 64 - 1);
     const uint32_t *src = p.qw + (int64_t)kb * (4 * (int64_t)p.N) + col64 * 256 + c0;
@@ -661,8 +661,9 @@ __device__ __forceinline__ void load_w(WRegs &r, const GParams &p, int32_t n0, i
 // k = 4h+2, 10+4h, 4h+3, 11+4h (bytes 0..3): k 4h..4h+3 go to half 0 at
 // element 4h, k 8+4h..11+4h to half 1 at element 4h.  Part e: the e-th of the
 // thread's four columns.
+template <int NG>
 __device__ __forceinline__ void store_w_part(const WRegs &r, uint16_t *ws, int tid, int e) {
-    const int band = tid >> 7, grp = (tid >> 5) & 3, idx = tid & 31;
+    const int band = tid / (32 * NG), grp = (tid >> 5) % NG, idx = tid & 31;
     const int n8 = idx >> 2, q = idx & 3;
     const int h = q >> 1;
     const int n = grp * 64 + ((q & 1) * 4 + e) * 8 + n8;  // column inside the tile
@@ -673,7 +674,7 @@ __device__ __forceinline__ void store_w_part(const WRegs &r, uint16_t *ws, int t
     const u32x2 lo = {pack_hi(a0, a2), pack_hi(b0, b2)};  // k 4h, 4h+1, 4h+2, 4h+3
     const u32x2 hi = {pack_hi(a1, a3), pack_hi(b1, b3)};  // k 8+4h .. 11+4h
     const int sw = (n >> 3) & 1;
-    uint16_t *col = ws + (band * TBN + n) * 16;
+    uint16_t *col = ws + (band * NG * 64 + n) * 16;
     *reinterpret_cast<u32x2 *>(col + (0 ^ sw) * 8 + 4 * h) = lo;
     *reinterpret_cast<u32x2 *>(col + (1 ^ sw) * 8 + 4 * h) = hi;
 }
@@ -692,19 +693,45 @@ __device__ __forceinline__ void wait_w(WRegs &r) {
 // tile kt run with the dequantized stores of W(kt+1) -- loaded a whole
 // iteration earlier -- between their k-steps; one counted wait for x(kt+1)
 // and W(kt+1), one barrier.
+//
+// The W loads are inline asm the compiler cannot see in flight: any copy of
+// their registers placed between a load and its wait would read stale data,
+// and the compiler places such copies where control flow merges.  So nothing
+// between a load and its wait branches: every iteration issues its copies and
+// loads (past the last k-tile they reread the last band and fill a stage no
+// one reads), every wait has the same count, K is a multiple of two k-tiles
+// (the loop body is two iterations with no test between them), and the last
+// loads are waited for, by a wait that names their registers, before the
+// epilogue reuses LDS and registers.
 constexpr int NXS = 3;
 
-template <int MODE>
-__global__ __launch_bounds__(512, 1) void w8a16_gemm_tile256_kernel(GParams p) {
+// TM x TM tiles: TM = 256 with eight waves (2 x 4, 128 x 64 a wave, 160 KB of
+// LDS, one workgroup a CU); TM = 128 with four (2 x 2, 64 x 64 a wave, 80 KB,
+// two a CU).  A thread issues four x copies and two W loads a k-tile in both.
+template <int TM>
+struct Pipe {
+    static constexpr int NT = TM == 256 ? 512 : 256;  // threads
+    static constexpr int WN = NT / 128;               // waves along n (2 along m)
+    static constexpr int NG = TM / 64;                // 64-column groups
+    static constexpr int TX = TM * BK;                // bf16 elements of one x image
+    static constexpr int TW = (BK / 16) * TM * 16;    // bf16 elements of one W image
+    static constexpr int WG_PER_CU = TM == 256 ? 1 : 2;
+};
+
+template <int MODE, int TM>
+__global__ __launch_bounds__(Pipe<TM>::NT, Pipe<TM>::WG_PER_CU) void w8a16_gemm_pipe_kernel(GParams p) {
+    using PP = Pipe<TM>;
+    constexpr int NT = PP::NT, NG = PP::NG, TX = PP::TX, TW = PP::TW, TBN = TM;
     __shared__ __attribute__((aligned(16))) uint16_t smem[NXS * TX + 2 * TW];
-    constexpr int BM = 256, MI = 4;
+    constexpr int BM = TM, MI = BM / 64;
+    static_assert(BM * 8 == 4 * NT && (BK / 16) * TM * 16 == 32 * NT, "four x copies and two W loads a thread");
     const int nwg = (int)gridDim.x;
     const int lin = (int)(blockIdx.x % 8) * (nwg / 8) + (int)(blockIdx.x / 8);
     if (lin >= p.m_tiles * p.n_tiles) return;
     const int mt = lin % p.m_tiles, nt = lin / p.m_tiles;
     const int32_t m0 = mt * BM, n0 = nt * TBN;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int wm = wave >> 2, wn = wave & 3;
+    const int wm = wave / PP::WN, wn = wave % PP::WN;
     const int lrow = lane & 31, lhi = lane >> 5;
 
     // x rows [m0, M) as one buffer: rows past M read as zeros
@@ -712,11 +739,11 @@ __global__ __launch_bounds__(512, 1) void w8a16_gemm_tile256_kernel(GParams p) {
     const uint32_t xbytes = (uint32_t)min<int64_t>((int64_t)(p.M - m0) * p.ldx * 2, 0xffffffffLL);
     const u32x4 xdesc = buf_desc(xb, xbytes);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
-    // copy i of this wave: granules (i*512 + wave*64 + lane) of the x image
+    // copy i of this wave: granules (i*NT + wave*64 + lane) of the x image
     uint32_t xoff[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int g = i * 512 + wave * 64 + lane;
+        const int g = i * NT + wave * 64 + lane;
         const int row = g >> 3, slot = g & 7;
         const int c = slot ^ ((row >> 1) & 7);
         xoff[i] = (uint32_t)((row * p.ldx + c * 8) * 2);
@@ -724,7 +751,7 @@ __global__ __launch_bounds__(512, 1) void w8a16_gemm_tile256_kernel(GParams p) {
     auto copy_x = [&](int stage, int32_t k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            lds_copy16(xdesc, lds0 + (uint32_t)(stage * TX + i * 512 * 8 + wave * 64 * 8) * 2,
+            lds_copy16(xdesc, lds0 + (uint32_t)(stage * TX + i * NT * 8 + wave * 64 * 8) * 2,
                        xoff[i] + (uint32_t)k0 * 2);
     };
     uint16_t *const wst = smem + NXS * TX;  // the two W images
@@ -735,31 +762,24 @@ __global__ __launch_bounds__(512, 1) void w8a16_gemm_tile256_kernel(GParams p) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-    const int32_t n_kt = p.K / BK;
+    const int32_t n_kt = p.K / BK;  // even
     WRegs wr[2];
     copy_x(0, 0);
-    load_w(wr[0], p, n0, 0, tid);
-    if (n_kt > 1) {
-        copy_x(1, BK);
-        load_w(wr[1], p, n0, BK, tid);
-        wait_w<6>(wr[0]);
-    } else {
-        wait_w<0>(wr[0]);
-    }
+    load_w<NG>(wr[0], p, n0, 0, tid);
+    copy_x(1, BK);
+    load_w<NG>(wr[1], p, n0, BK, tid);
+    wait_w<6>(wr[0]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) store_w_part(wr[0], wst, tid, e);
+    for (int e = 0; e < 4; ++e) store_w_part<NG>(wr[0], wst, tid, e);
     __syncthreads();
 
     // two iterations per trip so the W register set is a compile-time index
     auto iteration = [&](int32_t kt, auto par) __attribute__((always_inline)) {
         constexpr int P = decltype(par)::value;  // kt & 1
         const int xs_cur = kt % NXS;
-        const bool issue = kt + 2 < n_kt;
         const bool more = kt + 1 < n_kt;
-        if (issue) {
-            copy_x((kt + 2) % NXS, (kt + 2) * BK);
-            load_w(wr[P], p, n0, (kt + 2) * BK, tid);  // set P held W(kt), stored last iteration
-        }
+        copy_x((kt + 2) % NXS, (kt + 2) * BK);
+        load_w<NG>(wr[P], p, n0, (kt + 2) * BK, tid);  // set P held W(kt), stored last iteration
         const uint16_t *xs = smem + xs_cur * TX;
         const uint16_t *ws = wst + P * TW;
         uint16_t *ws_next = wst + (P ^ 1) * TW;
@@ -768,7 +788,7 @@ __global__ __launch_bounds__(512, 1) void w8a16_gemm_tile256_kernel(GParams p) {
         auto read_frags = [&](int ks, int buf) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
-                const int row = wm * 128 + i * 32 + lrow;
+                const int row = wm * (BM / 2) + i * 32 + lrow;
                 const int c = ks * 2 + lhi;
                 fa[buf][i] = __builtin_bit_cast(
                     bf16x8, *reinterpret_cast<const u32x4 *>(xs + (row * 8 + (c ^ ((row >> 1) & 7))) * 8));
@@ -790,32 +810,42 @@ __global__ __launch_bounds__(512, 1) void w8a16_gemm_tile256_kernel(GParams p) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][i], fb[cb][j], acc[i][j], 0, 0, 0);
-            if (more) {
-                if (ks == 0) {
-                    // x(kt+1) and W(kt+1) (issued before this iteration's copies) have landed
-                    if (issue)
-                        wait_w<6>(wr[P ^ 1]);
-                    else
-                        wait_w<0>(wr[P ^ 1]);
-                }
-                store_w_part(wr[P ^ 1], ws_next, tid, ks);
-            }
+            // x(kt+1) and W(kt+1) (issued before this iteration's copies) have landed
+            if (ks == 0) wait_w<6>(wr[P ^ 1]);
+            if (more) store_w_part<NG>(wr[P ^ 1], ws_next, tid, ks);
         }
         __syncthreads();
     };
     for (int32_t kt = 0; kt < n_kt; kt += 2) {
         iteration(kt, std::integral_constant<int, 0>{});
-        if (kt + 1 < n_kt) iteration(kt + 1, std::integral_constant<int, 1>{});
+        iteration(kt + 1, std::integral_constant<int, 1>{});
     }
-    gemm_epilogue<MODE, BM, 512>(p, acc, m0, n0, wm, wn, lane, smem);
+    // The copies and W loads issued past the last k-tile land here.  The wait
+    // names both W register sets: until it, they stay reserved for their
+    // loads (a plain wait would let the epilogue's address arithmetic take
+    // those registers while the loads could still overwrite them).
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(wr[0].w0), "+v"(wr[0].w1), "+v"(wr[1].w0), "+v"(wr[1].w1));
+    __syncthreads();
+    gemm_epilogue<MODE, BM, NT>(p, acc, m0, n0, wm, wn, lane, smem);
 }
 
-template <int MODE>
-hipError_t launch_tile256(const GParams &p, hipStream_t stream) {
+template <int MODE, int TM>
+hipError_t launch_pipe(const GParams &p, hipStream_t stream) {
     const int total = p.m_tiles * p.n_tiles;
     const int grid = (total + 7) / 8 * 8;
-    hipLaunchKernelGGL((w8a16_gemm_tile256_kernel<MODE>), dim3(grid), dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((w8a16_gemm_pipe_kernel<MODE, TM>), dim3(grid), dim3(Pipe<TM>::NT), 0, stream, p);
     return hipGetLastError();
+}
+
+template <int TM>
+hipError_t dispatch_pipe(const GParams &p, int mode, hipStream_t stream) {
+    switch (mode) {
+        case Y_BF16: return launch_pipe<Y_BF16, TM>(p, stream);
+        case Y_F32_ROUNDED: return launch_pipe<Y_F32_ROUNDED, TM>(p, stream);
+        case Y_F32_RAW: return launch_pipe<Y_F32_RAW, TM>(p, stream);
+        case Y_GATED: return launch_pipe<Y_GATED, TM>(p, stream);
+        default: return launch_pipe<Y_QKV, TM>(p, stream);
+    }
 }
 
 inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -924,17 +954,15 @@ int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
         p.ldx = p.K;
         xf32 = false;
     }
-    if (!dense && !xf32 && p.K % BK == 0 && !narrow && aligned16(p.x)) {
-        // 256 x 256 tiles, x copied straight into LDS
-        p.n_tiles = (p.N + TBN - 1) / TBN;
-        p.m_tiles = (p.M + 255) / 256;
-        switch (mode) {
-            case Y_BF16: e = launch_tile256<Y_BF16>(p, stream); break;
-            case Y_F32_ROUNDED: e = launch_tile256<Y_F32_ROUNDED>(p, stream); break;
-            case Y_F32_RAW: e = launch_tile256<Y_F32_RAW>(p, stream); break;
-            case Y_GATED: e = launch_tile256<Y_GATED>(p, stream); break;
-            default: e = launch_tile256<Y_QKV>(p, stream); break;
-        }
+    if (!dense && !xf32 && p.K % (2 * BK) == 0 && aligned16(p.x)) {
+        // x copied straight into LDS: 256 x 256 tiles when they fill at least
+        // three quarters of MI355X's 256 CUs (one a CU), 128 x 128 otherwise
+        // (two a CU)
+        const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
+        const int tm = t256 >= 192 ? 256 : 128;
+        p.n_tiles = (p.N + tm - 1) / tm;
+        p.m_tiles = (p.M + tm - 1) / tm;
+        e = tm == 256 ? dispatch_pipe<256>(p, mode, stream) : dispatch_pipe<128>(p, mode, stream);
     } else {
         e = narrow ? dispatch<128>(p, xf32, mode, stream) : dispatch<256>(p, xf32, mode, stream);
     }

@@ -97,6 +97,29 @@ def test_w8_exact_integer_layout(emb, orc, torch_dev, M, K, N):
     assert np.array_equal(yr, orc.bf16_to_f32(yb_ref))
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (33, 128, 256),      # 128 x 128 pipelined tiles, two k-tiles
+    (200, 256, 320),     # 128 x 128, four k-tiles, a partial column group
+    (1792, 128, 7168),   # 256 x 256 pipelined tiles (196 of them), two k-tiles
+    (33, 64, 256),       # one k-tile: the single-stage kernel
+])
+def test_w8_pipeline_k_tiles(emb, orc, torch_dev, M, K, N):
+    """Exact integer products at the fewest k-tiles each kernel runs: the loads
+    issued past the last k-tile and the drain before the epilogue must leave
+    the result unchanged; bf16 output through the QKV-free epilogue too."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(M + K + N)
+    w = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    q = orc.marlin_pack_w8(w)
+    s_st = orc.marlin_pack_scales(orc.f32_to_bf16((2.0 ** rng.integers(-10, -3, N)).astype(np.float32)))
+    x = orc.f32_to_bf16(rng.integers(-4, 5, (M, K)).astype(np.float32))
+    yb_ref, yf_ref = orc.w8a16_gemm(x, q, s_st, M, K, N)
+    yf = _gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_F32_RAW)
+    bad = np.argwhere(yf != yf_ref)
+    assert not len(bad), f"{len(bad)} of {M * N} differ, first {bad[:4].tolist()}"
+    assert np.array_equal(_gemm(emb, torch, dev, x, q, s_st, M, K, N, emb.EMB_W8_Y_BF16), yb_ref)
+
+
 def test_w8_scale_permutation_exact(emb, orc, torch_dev):
     """Power-of-two per-channel scales keep the result exact and make a wrong
     scale permutation visible column by column."""
