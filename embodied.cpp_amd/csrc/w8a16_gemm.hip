@@ -829,6 +829,115 @@ __global__ __launch_bounds__(Pipe<TM>::NT, Pipe<TM>::WG_PER_CU) void w8a16_gemm_
     gemm_epilogue<MODE, BM, NT>(p, acc, m0, n0, wm, wn, lane, smem);
 }
 
+// ---- Dense bf16 weights: both operands copied straight into LDS ----
+//
+// ggml BF16 weights are [N][K] rows, the layout of x, so a W tile is staged
+// like an x tile: DMA copies into a two-stage ring (x keeps its three), B
+// fragments read with the same granule swizzle.  Per k-tile kt: the copies of
+// W(kt+1) and then of x(kt+2) go out; the MFMAs of tile kt run; vmcnt(4)
+// (everything but the x copies just issued) and one barrier.  No register
+// loads, so nothing is in flight in registers.
+template <int TM>
+__global__ __launch_bounds__(Pipe<TM>::NT, Pipe<TM>::WG_PER_CU) void dense_gemm_pipe_kernel(GParams p) {
+    using PP = Pipe<TM>;
+    constexpr int NT = PP::NT, TX = PP::TX;  // a W image is TM rows x BK too
+    constexpr int NWS = 2;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[NXS * TX + NWS * TX];
+    constexpr int BM = TM, MI = BM / 64;
+    static_assert(BM * 8 == 4 * NT, "four copies a thread for each operand");
+    const int nwg = (int)gridDim.x;
+    const int lin = (int)(blockIdx.x % 8) * (nwg / 8) + (int)(blockIdx.x / 8);
+    if (lin >= p.m_tiles * p.n_tiles) return;
+    const int mt = lin % p.m_tiles, nt = lin / p.m_tiles;
+    const int32_t m0 = mt * BM, n0 = nt * TM;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = wave / PP::WN, wn = wave % PP::WN;
+    const int lrow = lane & 31, lhi = lane >> 5;
+
+    // rows past M (x) or N (W) read as zeros
+    const uint16_t *xb = reinterpret_cast<const uint16_t *>(p.x) + (int64_t)m0 * p.ldx;
+    const u32x4 xdesc = buf_desc(xb, (uint32_t)min<int64_t>((int64_t)(p.M - m0) * p.ldx * 2, 0xffffffffLL));
+    const uint16_t *wb = reinterpret_cast<const uint16_t *>(p.wd) + (int64_t)n0 * p.ldw;
+    const u32x4 wdesc = buf_desc(wb, (uint32_t)min<int64_t>((int64_t)(p.N - n0) * p.ldw * 2, 0xffffffffLL));
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
+    uint32_t xoff[4], woff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int g = i * NT + wave * 64 + lane;
+        const int row = g >> 3, c = (g & 7) ^ ((row >> 1) & 7);
+        xoff[i] = (uint32_t)((row * p.ldx + c * 8) * 2);
+        woff[i] = (uint32_t)((row * p.ldw + c * 8) * 2);
+    }
+    auto copy = [&](const u32x4 &desc, const uint32_t (&off)[4], int base, int32_t k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            lds_copy16(desc, lds0 + (uint32_t)(base + i * NT * 8 + wave * 64 * 8) * 2, off[i] + (uint32_t)k0 * 2);
+    };
+    auto copy_x = [&](int stage, int32_t k0) { copy(xdesc, xoff, stage * TX, k0); };
+    auto copy_w = [&](int stage, int32_t k0) { copy(wdesc, woff, (NXS + stage) * TX, k0); };
+
+    f32x16 acc[MI][2];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+    const int32_t n_kt = p.K / BK;
+    copy_w(0, 0);
+    copy_x(0, 0);
+    if (n_kt > 1) copy_x(1, BK);
+    wait_vmcnt<0>();
+    __syncthreads();
+    for (int32_t kt = 0; kt < n_kt; ++kt) {
+        const bool more = kt + 1 < n_kt, more2 = kt + 2 < n_kt;
+        if (more) copy_w((kt + 1) % NWS, (kt + 1) * BK);
+        if (more2) copy_x((kt + 2) % NXS, (kt + 2) * BK);
+        const uint16_t *xs = smem + (kt % NXS) * TX;
+        const uint16_t *ws = smem + (NXS + kt % NWS) * TX;
+        bf16x8 fa[2][MI], fb[2][2];
+        auto read_frags = [&](int ks, int buf) __attribute__((always_inline)) {
+            const int c = ks * 2 + lhi;
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int row = wm * (BM / 2) + i * 32 + lrow;
+                fa[buf][i] = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4 *>(xs + (row * 8 + (c ^ ((row >> 1) & 7))) * 8));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = wn * 64 + j * 32 + lrow;
+                fb[buf][j] = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4 *>(ws + (n * 8 + (c ^ ((n >> 1) & 7))) * 8));
+            }
+        };
+        read_frags(0, 0);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int cb = ks & 1;
+            if (ks + 1 < BK / 16) read_frags(ks + 1, cb ^ 1);
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][i], fb[cb][j], acc[i][j], 0, 0, 0);
+        }
+        // W(kt+1) and x(kt+1) have landed (only the x(kt+2) copies may fly)
+        if (more2)
+            wait_vmcnt<4>();
+        else
+            wait_vmcnt<0>();
+        __syncthreads();
+    }
+    gemm_epilogue<Y_GATED_B16, BM, NT>(p, acc, m0, n0, wm, wn, lane, smem);
+}
+
+template <int TM>
+hipError_t launch_dense_pipe(const GParams &p, hipStream_t stream) {
+    const int total = p.m_tiles * p.n_tiles;
+    hipLaunchKernelGGL((dense_gemm_pipe_kernel<TM>), dim3((total + 7) / 8 * 8), dim3(Pipe<TM>::NT), 0, stream, p);
+    return hipGetLastError();
+}
+
 template <int MODE, int TM>
 hipError_t launch_pipe(const GParams &p, hipStream_t stream) {
     const int total = p.m_tiles * p.n_tiles;
@@ -954,7 +1063,14 @@ int run_gemm(GParams p, bool xf32, int mode, hipStream_t stream) {
         p.ldx = p.K;
         xf32 = false;
     }
-    if (!dense && !xf32 && p.K % (2 * BK) == 0 && aligned16(p.x)) {
+    if (dense && !xf32 && p.K % BK == 0 && p.ldw % 8 == 0 && aligned16(p.x) && aligned16(p.wd)) {
+        // both operands copied straight into LDS (tile size as below)
+        const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
+        const int tm = t256 >= 192 ? 256 : 128;
+        p.n_tiles = (p.N + tm - 1) / tm;
+        p.m_tiles = (p.M + tm - 1) / tm;
+        e = tm == 256 ? launch_dense_pipe<256>(p, stream) : launch_dense_pipe<128>(p, stream);
+    } else if (!dense && !xf32 && p.K % (2 * BK) == 0 && aligned16(p.x)) {
         // x copied straight into LDS: 256 x 256 tiles when they fill at least
         // three quarters of MI355X's 256 CUs (one a CU), 128 x 128 otherwise
         // (two a CU)

@@ -72,19 +72,27 @@ def _lin(emb, torch, dev, xt, wt, wtype, M, K, N, x_is_f32=True, ldx=None, ws=No
     return out
 
 
-@pytest.mark.parametrize("bf16w", [True, False], ids=["bf16", "f32"])
+@pytest.mark.parametrize("bf16w,xform", [(True, "f32"), (True, "bf16"), (False, "f32")],
+                         ids=["bf16-staged", "bf16-copied", "f32"])
 @pytest.mark.parametrize("M,K,N,sample", [
     (300, 512, 384, None),
     (129, 384, 200, None),       # N not a multiple of the tile width
     (37, 1024, 64, None),
     (1560, 3072, 3072, 96),      # LingBot O-projection shape, sampled rows
 ])
-def test_dense_projection(emb, orc, torch_dev, bf16w, M, K, N, sample):
+def test_dense_projection(emb, orc, torch_dev, bf16w, xform, M, K, N, sample):
+    """xform "f32": x rounded while staged (the single-stage kernel); "bf16":
+    x given as bf16 rows, both operands copied straight into LDS."""
     torch, dev = torch_dev
     rng = np.random.default_rng(M * 7 + K + N + bf16w)
     x, w = _problem(orc, rng, M, K, N, bf16w)
     wtype = emb.EMB_GGML_BF16 if bf16w else emb.EMB_GGML_F32
-    out = _lin(emb, torch, dev, _t(torch, dev, x), _t(torch, dev, w), wtype, M, K, N)
+    if xform == "bf16":
+        x = orc.bf16_to_f32(orc.f32_to_bf16(x))  # the oracle rounds it the same way
+        out = _lin(emb, torch, dev, _t(torch, dev, orc.f32_to_bf16(x)), _t(torch, dev, w), wtype, M, K, N,
+                   x_is_f32=False)
+    else:
+        out = _lin(emb, torch, dev, _t(torch, dev, x), _t(torch, dev, w), wtype, M, K, N)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     rows = np.arange(M) if sample is None else np.sort(rng.choice(M, sample, replace=False))
@@ -98,11 +106,16 @@ def test_dense_projection_bf16_wide(emb, orc, torch_dev):
     rng = np.random.default_rng(9216)
     M, K, N = 1560, 3072, 9216
     x, w = _problem(orc, rng, M, K, N, True)
-    out = _lin(emb, torch, dev, _t(torch, dev, x), _t(torch, dev, w), emb.EMB_GGML_BF16, M, K, N)
+    xb = orc.f32_to_bf16(x)
+    staged = _lin(emb, torch, dev, _t(torch, dev, x), _t(torch, dev, w), emb.EMB_GGML_BF16, M, K, N)
+    copied = _lin(emb, torch, dev, _t(torch, dev, xb), _t(torch, dev, w), emb.EMB_GGML_BF16, M, K, N,
+                  x_is_f32=False)
     torch.cuda.synchronize()
     rows = np.sort(rng.choice(M, 32, replace=False))
     rows[-1] = M - 1  # the last, partial row tile
-    _check_projection(orc, out.cpu().numpy()[rows], x, w, True, rows)
+    _check_projection(orc, staged.cpu().numpy()[rows], x, w, True, rows)
+    # the 256 x 256 copied-operand kernel sums the same k-steps in the same order
+    assert torch.equal(staged, copied), "staged and copied kernels differ"
 
 
 @pytest.mark.parametrize("bf16w", [True, False], ids=["bf16", "f32"])
