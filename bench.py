@@ -143,9 +143,12 @@ class PagedLayers:
         self.ws = None
         torch.cuda.synchronize()
 
-    def set_splits(self, splits, split_keys=0):
+    def set_splits(self, splits, split_keys=0, kernel=None):
+        """Split-K factor and kernel (embkv.EMB_ATTN_*; None: the row tiles, which
+        every split factor runs on)."""
         self.splits = splits
         self.split_keys = split_keys
+        self.kernel = self.c.emb.EMB_ATTN_ROW_TILES if kernel is None else kernel
         if splits > 1:
             nb = self.c.emb.attn_workspace_bytes(self.L, self.n_new, self.hq, self.hkv, self.d, splits)
             self.ws = self.c.torch.zeros(nb // 4 + 64, dtype=self.c.torch.float32, device=self.c.dev)
@@ -166,7 +169,8 @@ class PagedLayers:
                                    n_keys=None if self.uniform else self.nk,
                                    n_keys_uniform=self.n_keys[0] if self.uniform else 0,
                                    block_tables=self.bt, bt_stride=self.bt_stride, splits=self.splits,
-                                   workspace=self.ws, stream=stream, split_keys=getattr(self, "split_keys", 0))
+                                   workspace=self.ws, stream=stream, split_keys=getattr(self, "split_keys", 0),
+                                   kernel=getattr(self, "kernel", 0))
 
     # algorithmic bytes of one attention launch: K/V of every key once, Q, O (f32), tables
     def attn_bytes(self):
@@ -188,19 +192,34 @@ class PagedLayers:
         return b
 
 
+def kernel_choices(c: Ctx, splits_list):
+    """(label, kernel, splits) candidates: the key-split kernel, then the row
+    tiles at each split factor."""
+    emb = c.emb
+    return [("key_split", emb.EMB_ATTN_KEY_SPLIT, 1)] + [(f"row_tiles_split{sp}", emb.EMB_ATTN_ROW_TILES, sp)
+                                                          for sp in splits_list]
+
+
 def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
     n_layers, n_pref, n_new, hq, hkv, d = 18, 816, 51, 8, 1, 256
     P = PagedLayers(c, 0xE3BD0000, [n_pref] * n_layers, n_new, hq, hkv, d, n_steps=10)
     scale = 1.0 / math.sqrt(d)
     best = None
     sweep = {}
-    for sp in splits_list:
-        P.set_splits(sp)
-        ms, _ = c.time_graph(lambda st: P.attend(0, st, scale), steps, warmup)
-        sweep[sp] = ms * 1e3
+    # each candidate timed as 10 launches in one graph (a launch alone is
+    # dominated by the graph launch itself, which the denoise-step graph pays
+    # once for all its launches)
+    def ten(st):
+        for i in range(10):
+            P.attend(i, st, scale)
+    for label, kern, sp in kernel_choices(c, splits_list):
+        P.set_splits(sp, kernel=kern)
+        ms10, _ = c.time_graph(ten, max(2, steps // 4), 2)
+        ms = ms10 / 10
+        sweep[label] = ms * 1e3
         if best is None or ms < best[1]:
-            best = (sp, ms)
-    P.set_splits(best[0])
+            best = ((sp, kern, label), ms)
+    P.set_splits(best[0][0], kernel=best[0][1])
     attn_us = best[1] * 1e3
     # K consecutive attention launches in one graph: the kernel's average duration
     k_launch = 20
@@ -246,12 +265,13 @@ def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
         for _ in range(k_launch):
             single.attend(0, st, scale)
     sweep1 = {}
-    for sp in (1, 2, 4, 8, 16):
-        single.set_splits(sp)
+    choices1 = {lab: (kern, sp) for lab, kern, sp in kernel_choices(c, (1, 2, 4, 8, 16))}
+    for lab, (kern, sp) in choices1.items():
+        single.set_splits(sp, kernel=kern)
         ms1, _ = c.time_graph(single_many, max(2, steps // 4), 2)
-        sweep1[sp] = ms1 * 1e3 / k_launch
+        sweep1[lab] = ms1 * 1e3 / k_launch
     best1 = min(sweep1, key=sweep1.get)
-    single.set_splits(best1)
+    single.set_splits(choices1[best1][1], kernel=choices1[best1][0])
 
     # dependent per-layer launches (model-realistic ordering): 18 x (append, attention)
     layers = [single] * n_layers  # same shapes; the graph holds 36 dependent launches
@@ -299,16 +319,17 @@ def bench_cfg1(c: Ctx, steps, warmup, splits_list=(1, 2, 3, 4, 8)):
         us_per_step_10step_graph=ms_ten * 1e3 / 10,
         us_per_step_dependent_layers=ms_layer * 1e3,
         attn_us_single_layer=sweep1[best1],
-        single_layer_splits=best1,
+        single_layer_kernel=best1,
         single_layer_split_sweep_us=sweep1,
         us_per_step_with_neox_producer=ms_prod_step * 1e3,
         neox_producer_us=ms_prod * 1e3,
         neox_producer_bytes=prod_bytes,
         neox_producer_gbs=prod_bytes / (ms_prod * 1e-3) / 1e9,
-        attn_us_single_launch=attn_us,
+        attn_us_in_sweep=attn_us,
         attn_us_avg_in_graph=attn_avg_us,
-        splits=best[0],
-        split_sweep_us=sweep,
+        splits=best[0][0],
+        kernel=best[0][2],
+        kernel_sweep_us=sweep,
         attn_bytes_per_launch=ab,
         attn_flops_per_launch=P.attn_flops(),
         survey_bytes_per_step=P.survey_step_bytes(),
@@ -350,17 +371,21 @@ def bench_cfg4(c: Ctx, steps, warmup):
         P = PagedLayers(c, 0xE3BD0004 + B, lens_all[:B], 51, 8, 1, 256, n_steps=2)
         # (splits, split_keys): uniform splits, and per-session splits sized
         # by each session's key count (split_keys > 0)
+        # and the key-split kernel (one workgroup per 32 rows, no split)
         best = None
         sweep = {}
-        for sp, sk in ((1, 0), (2, 0), (4, 0), (8, 0), (3, 384), (4, 256), (4, 320), (6, 192), (8, 128)):
+        ks = c.emb.EMB_ATTN_KEY_SPLIT
+        for sp, sk, kern in ((1, 0, ks), (1, 0, None), (2, 0, None), (4, 0, None), (8, 0, None), (3, 384, None),
+                             (4, 256, None), (4, 320, None), (6, 192, None), (8, 128, None)):
             if B >= 32 and sk == 0 and sp > 2:
                 continue
-            P.set_splits(sp, sk)
+            P.set_splits(sp, sk, kernel=kern)
             ms, _ = c.time_graph(lambda st: P.attend(0, st, 1 / 16), steps, warmup)
-            sweep[f"{sp}/{sk}"] = ms * 1e3
+            label = "key_split" if kern == ks else f"{sp}/{sk}"
+            sweep[label] = ms * 1e3
             if best is None or ms < best[1]:
-                best = ((sp, sk), ms)
-        P.set_splits(*best[0])
+                best = ((sp, sk, kern, label), ms)
+        P.set_splits(best[0][0], best[0][1], kernel=best[0][2])
 
         def one(st):
             P.append(0, st)
@@ -368,7 +393,7 @@ def bench_cfg4(c: Ctx, steps, warmup):
         ms_all, _ = c.time_graph(one, steps, warmup)
         ab = P.attn_bytes()
         res[f"B{B}"] = dict(attn_us=best[1] * 1e3, append_plus_attn_us=ms_all * 1e3, splits=best[0][0],
-                            split_keys=best[0][1], split_sweep_us=sweep,
+                            split_keys=best[0][1], kernel=best[0][3], split_sweep_us=sweep,
                             attn_gbs=ab / (best[1] * 1e-3) / 1e9,
                             attn_hbm_frac=ab / (best[1] * 1e-3) / 1e9 / PEAK_HBM_GBS,
                             survey_bytes=P.survey_step_bytes(),
@@ -920,8 +945,9 @@ def _pmc_kib_per_dispatch(path: Path, kernel_sub: str, counter: str) -> float:
 def traffic_summary(root: Path):
     """HBM bytes per launch of the config-1 attention kernel from FETCH_SIZE / WRITE_SIZE (KiB per
     dispatch), each scaled by what the same counter reads for a plain device copy of known size."""
-    fa = _pmc_kib_per_dispatch(root / "pmc_fetch_attn", "paged_attn_kernel", "FETCH_SIZE")
-    wa = _pmc_kib_per_dispatch(root / "pmc_write_attn", "paged_attn_kernel", "WRITE_SIZE")
+    ksub = "attn_ks_kernel"  # the key-split kernel, the config-1 choice (bench --only cfg1_attn default)
+    fa = _pmc_kib_per_dispatch(root / "pmc_fetch_attn", ksub, "FETCH_SIZE")
+    wa = _pmc_kib_per_dispatch(root / "pmc_write_attn", ksub, "WRITE_SIZE")
     fc = _pmc_kib_per_dispatch(root / "pmc_fetch_copy", "copyBuffer", "FETCH_SIZE")
     wc = _pmc_kib_per_dispatch(root / "pmc_write_copy", "copyBuffer", "WRITE_SIZE")
     kf, kw = fc * 1024 / COPY_CALIB_BYTES, wc * 1024 / COPY_CALIB_BYTES
@@ -930,8 +956,8 @@ def traffic_summary(root: Path):
            "-- python3 /root/repo/bench.py --only {W} --steps 20 --warmup 2")
     text = f"""# Config-1 attention kernel: HBM traffic per launch (rocprofv3 PMC)
 
-Kernel: `paged_attn_kernel<256, FULL, DMA>` (config 1: 18 layers x 51 queries x 8 heads over 867 keys,
-head_dim 256, split-K 3), launched by `bench.py --only cfg1_attn`.
+Kernel: `attn_ks_kernel<256>` (the key-split kernel; config 1: 18 layers x 51 queries x 8 heads over
+867 keys, head_dim 256, one launch, no split-K), launched by `bench.py --only cfg1_attn`.
 
 | pass | command | mean per dispatch |
 |---|---|---|
@@ -953,11 +979,15 @@ traffic_bytes_per_launch: {traffic:.0f}
     print(text)
 
 
-def read_traffic():
-    """HBM bytes per launch from the committed PMC summary, or None."""
+def read_traffic(kernel_sub):
+    """HBM bytes per launch from the committed PMC summary, or None when the
+    summary does not cover kernel_sub (the kernel the headline ran)."""
     f = ROOT / "profiles" / TRAFFIC_FILE
     try:
-        for line in f.read_text().splitlines():
+        text = f.read_text()
+        if kernel_sub not in text:
+            return None
+        for line in text.splitlines():
             if line.startswith("traffic_bytes_per_launch:"):
                 return float(line.split(":", 1)[1])
     except OSError:
@@ -998,8 +1028,12 @@ def main():
         log("profile loop done")
         return
     if args.only == "cfg1_attn":
+        # EMB_KERNEL=key_split (default) or row_tiles (with EMB_SPLITS, default 3)
         P = PagedLayers(c, 0xE3BD0000, [816] * 18, 51, 8, 1, 256, n_steps=10)
-        P.set_splits(int(os.environ.get("EMB_SPLITS", "3")))
+        if os.environ.get("EMB_KERNEL", "key_split") == "key_split":
+            P.set_splits(1, kernel=c.emb.EMB_ATTN_KEY_SPLIT)
+        else:
+            P.set_splits(int(os.environ.get("EMB_SPLITS", "3")))
         for i in range(args.warmup + args.steps):
             P.attend(i, c.stream, 1 / 16)
         c.torch.cuda.synchronize()
@@ -1013,11 +1047,12 @@ def main():
         c.torch.cuda.synchronize()
         log("profile loop done")
         return
-    if args.only == "cfg4_attn":  # B = 64 sessions, one layer, split 1
+    if args.only == "cfg4_attn":  # B = 64 sessions, one layer, unsplit (EMB_KERNEL as for cfg1_attn)
         g = MT64(0xE3BD0004)
         lens = [300 + g.next() % 901 for _ in range(64)]
         P = PagedLayers(c, 0xE3BD0004 + 64, lens, 51, 8, 1, 256, n_steps=2)
-        P.set_splits(1)
+        P.set_splits(1, kernel=c.emb.EMB_ATTN_KEY_SPLIT
+                     if os.environ.get("EMB_KERNEL", "key_split") == "key_split" else None)
         for _ in range(args.warmup + args.steps):
             P.attend(0, c.stream, 1 / 16)
         c.torch.cuda.synchronize()
@@ -1094,10 +1129,13 @@ def main():
                                "layers batched in one launch; `steps` consecutive steps timed as one "
                                "HIP-graph replay",
                    "layers": 18, "prefix": 816, "queries": 51, "hq": 8, "hkv": 1, "head_dim": 256,
-                   "page_tokens": 16, "splits": r1["splits"]},
+                   "page_tokens": 16, "kernel": r1["kernel"], "splits": r1["splits"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": read_traffic(),
-                     "kernel": ("paged_attn_kernel<256,FULL,DMA>" +
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": read_traffic("attn_ks_kernel" if r1["kernel"] == "key_split"
+                                                                        else "paged_attn_kernel"),
+                     "kernel": ("attn_ks_kernel<256> (key-split workgroups, one launch)"
+                                if r1["kernel"] == "key_split" else
+                                "paged_attn_kernel<256,FULL,DMA>" +
                                 (f" + attn_merge_kernel<256> (one split-K {r1['splits']} attention launch)"
                                  if r1["splits"] > 1 else "")),
                      "kernel_us": kern_us,

@@ -62,6 +62,7 @@
 #include <mutex>
 #include <type_traits>
 
+#include "attn_dev.h"
 #include "emb_common.h"
 
 // Split-K scratch of emb_paged_attention_noalloc: the partials of a call live
@@ -72,25 +73,12 @@ static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+using namespace emb_attn;
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int WAVES = 4;
 constexpr int ROWS_PER_WAVE = 32;
 constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
-constexpr float RESCALE_TH = 8.0f;  // log2 units
-// A row whose largest |O| lies below this (with a non-empty key set) is
-// recomputed exactly from the bf16 pool (see the epilogue).
-constexpr float EXACT_TINY = 0x1p-12f;
-constexpr float LOG2E = 1.4426950408889634f;
 constexpr int SEG_PAGES = 1024;  // block-table entries held in LDS at a time (16384 keys)
 // Block-table entries every wave of the DMA path holds in registers from the start.
 constexpr int WIN_PAGES = 128;
@@ -98,7 +86,6 @@ constexpr int WIN_PAGES = 128;
 // LDS latency is several MFMA issue slots, and the compiler's own schedule
 // issues each read just one MFMA ahead.
 constexpr int AHEAD = 4;
-constexpr uint32_t RSRC_W3 = 0x00020000u;  // buffer resource word 3 (raw, 32-bit elements)
 
 enum { LD_DMA = 0, LD_REG = 1, LD_VALID = 2 };
 
@@ -160,42 +147,6 @@ struct KParams {
     uint16_t *ws_o;
     float *ws_ml;    // [batch*hkv][splits][row_tiles*128][4]: m (log2 units), l, k (O/l stored as O/l * 2^-k), 0
 };
-
-__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
-
-// Four floats as four f16 (round to nearest even), packed in two dwords.
-__device__ __forceinline__ u32x2 f16x4_bits(const f32x4 &v) {
-    u32x2 w;
-    w[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[0]) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[1]) << 16);
-    w[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2]) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[3]) << 16);
-    return w;
-}
-
-// Lane l and lane l ^ 32 of x, as a pair, by one VALU lane swap: the first
-// element is x of lane l & 31, the second x of lane l | 32 (so their max or
-// sum is the same in both halves of the wave).
-__device__ __forceinline__ void half_pair(float x, float &a, float &b) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
-                                                    false, false);
-    a = __builtin_bit_cast(float, (uint32_t)r[0]);
-    b = __builtin_bit_cast(float, (uint32_t)r[1]);
-}
-
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-}
-
-// The four values rounded to bf16 precision (nearest even), kept as f32.
-__device__ __forceinline__ f32x4 round_bf16x4(const f32x4 &v) {
-    return f32x4{__builtin_bit_cast(float, f32_to_bf16_bits(v[0]) << 16),
-                 __builtin_bit_cast(float, f32_to_bf16_bits(v[1]) << 16),
-                 __builtin_bit_cast(float, f32_to_bf16_bits(v[2]) << 16),
-                 __builtin_bit_cast(float, f32_to_bf16_bits(v[3]) << 16)};
-}
 
 // Two bf16 (packed in a dword) -> two f16 (packed in a dword), round to nearest even.
 __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
@@ -260,39 +211,6 @@ __device__ __forceinline__ void page_rsrc(const KParams &p, const uint16_t *vbas
     }
 }
 
-// Raw buffer descriptor over [base, base + bytes) (stride 0, 32-bit records),
-// its words forced into SGPRs (the arguments are wave-uniform).
-__device__ __forceinline__ u32x4 buf_desc(const void *base, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
-                 (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
-                 (uint32_t)__builtin_amdgcn_readfirstlane(bytes), RSRC_W3};
-}
-
-// vmcnt(N) with the other counters left alone.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
-}
-
-// One global -> LDS copy of 16 bytes a lane: lane i's 16 bytes at byte offset
-// voff of the buffer land at LDS byte m0 + 16 i (bytes past the buffer's end
-// land as zeros).  Written as inline asm on purpose: the compiler cannot tell
-// the pipeline stages apart, so for its own form of this load it waits for
-// every outstanding copy (vmcnt(0)) before the next LDS read of any stage --
-// the prefetch included.  The kernel counts these loads itself (wait_vmcnt).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_copy16(const u32x4 &desc, uint32_t m0, uint32_t voff) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"  // SALU write of M0 -> LDS-DMA read of M0: one wait state
-        "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0),
-        "v"(voff), "s"(desc)
-        : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 // DMA path: the tile's K rows and f16 V-shadow pages go straight into the
 // stage.  Wave w copies 1 KB blocks b = 4j + w of each image; block b of the
@@ -1656,6 +1574,15 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     }
     const bool qf32 = a->q_is_f32 != 0;
     hipError_t e;
+    EMB_CHECK_ARG(a->kernel >= EMB_ATTN_AUTO && a->kernel <= EMB_ATTN_KEY_SPLIT, "unknown kernel choice");
+    const bool ks_ok = a->mask_kind == EMB_MASK_FULL && a->v16_pool && !a->valid_slots && !a->p_bf16 &&
+                       (a->head_dim == 128 || a->head_dim == 256) && splits == 1 &&
+                       (!a->block_tables || a->bt_stride <= KS_MAX_PAGES);
+    if (a->kernel == EMB_ATTN_KEY_SPLIT && !ks_ok)
+        return emb::set_error(EMB_ERR_UNSUPPORTED,
+                              "the key-split kernel takes the FULL mask, an f16 V shadow, no valid-slot list, "
+                              "head_dim 128 or 256, no split-K, no p_bf16 and at most %d block-table entries",
+                              KS_MAX_PAGES);
     if (a->p_bf16) {
         EMB_CHECK_ARG(splits == 1, "p_bf16 runs unsplit (splits must be 0 or 1)");
         EMB_CHECK_ARG(a->mask_kind != EMB_MASK_BLOCKMAP, "p_bf16 takes no block map");
@@ -1667,6 +1594,36 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
             default: e = dispatch_pbf16<256>(kp, a->mask_kind, valid, qf32, stream); break;
         }
         if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "p_bf16 attention launch: %s", hipGetErrorString(e));
+        return EMB_OK;
+    }
+    const int64_t rows_per_unit = (int64_t)a->max_q * kp.G;
+    if (ks_ok && (a->kernel == EMB_ATTN_KEY_SPLIT || (a->kernel == EMB_ATTN_AUTO && rows_per_unit <= 512))) {
+        KsParams ks{};
+        ks.q = kp.q;
+        ks.out = kp.out;
+        ks.q_stride = kp.q_stride;
+        ks.out_stride = kp.out_stride;
+        ks.round_out = kp.round_out;
+        ks.cu_q = kp.cu_q;
+        ks.n_keys = kp.n_keys;
+        ks.nq_single = kp.nq_single;
+        ks.nk_single = kp.nk_single;
+        ks.k_pool = kp.k_pool;
+        ks.v_pool = kp.v_pool;
+        ks.v16_pool = kp.v16_pool;
+        ks.bt = kp.bt;
+        ks.bt_stride = kp.bt_stride;
+        ks.capacity = kp.capacity;
+        ks.hkv = kp.hkv;
+        ks.G = kp.G;
+        ks.row_blocks = (int32_t)((rows_per_unit + 31) / 32);
+        const int64_t wgs = (int64_t)a->batch * a->hkv * ks.row_blocks;
+        EMB_CHECK_ARG(wgs < INT_MAX / 2, "grid too large");
+        ks.total_wg = (int32_t)wgs;
+        ks.c_log2 = kp.c_log2;
+        ks.th_raw = kp.th_raw;
+        e = ks_launch(ks, a->head_dim, qf32, stream);
+        if (e != hipSuccess) return emb::set_error(EMB_ERR_LAUNCH, "key-split attention launch: %s", hipGetErrorString(e));
         return EMB_OK;
     }
     const int ld = a->valid_slots ? LD_VALID : (a->v16_pool ? LD_DMA : LD_REG);

@@ -18,6 +18,7 @@ LIB_PATH = PKG / "libemb_kv.so"
 _lib = None
 
 EMB_MASK_FULL, EMB_MASK_CHUNK, EMB_MASK_TOKEN, EMB_MASK_ADD, EMB_MASK_BLOCKMAP = range(5)
+EMB_ATTN_AUTO, EMB_ATTN_ROW_TILES, EMB_ATTN_KEY_SPLIT = range(3)
 EMB_ERR_ARG, EMB_ERR_LAUNCH, EMB_ERR_CAPACITY, EMB_ERR_UNSUPPORTED = -1, -2, -3, -4
 
 i32p = C.POINTER(C.c_int32)
@@ -46,6 +47,7 @@ class AttnArgs(C.Structure):
         ("out_bf16_round", C.c_int32),
         ("p_bf16", C.c_int32),
         ("split_keys", C.c_int32),
+        ("kernel", C.c_int32),
     ]
 
 
@@ -578,7 +580,7 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
                     mask_q_stride=0, mask_batch_stride=0, block_map=None, block_size=0,
                     block_map_cols=0, block_map_batch_stride=0, splits=1, workspace=None,
                     n_keys_uniform=0, out_bf16_round=False, stream=None, noalloc=False, p_bf16=False,
-                    split_keys=0):
+                    split_keys=0, kernel=0):
     a = AttnArgs()
     a.q = ptr(q); a.q_is_f32 = int(q_is_f32)
     a.q_stride = q_stride if q_stride is not None else hq * d
@@ -597,6 +599,7 @@ def paged_attention(*, q, out, k_pool, v_pool, batch, hq, hkv, d, max_q, scale, 
     a.out_bf16_round = int(out_bf16_round)
     a.p_bf16 = int(p_bf16)
     a.split_keys = int(split_keys)
+    a.kernel = int(kernel)
     if noalloc:  # split-K partials in the library's scratch (workspace must be None)
         return check(lib().emb_paged_attention_noalloc(C.byref(a), stream_ptr(stream)), "emb_paged_attention_noalloc")
     return check(lib().emb_paged_attention(C.byref(a), stream_ptr(stream)), "emb_paged_attention")

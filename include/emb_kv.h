@@ -416,7 +416,28 @@ typedef struct emb_attn_args {
                                           min(splits, ceil(n / split_keys)) (at least 1), so
                                           short sequences of a ragged batch are not cut into
                                           splits that cost more than they save */
+    int32_t kernel;                    /* EMB_ATTN_AUTO (0), EMB_ATTN_ROW_TILES (1) or
+                                          EMB_ATTN_KEY_SPLIT (2), below */
 } emb_attn_args;
+
+/* emb_attn_args.kernel.  Both kernels compute the same attention; they differ
+ * in how the work is cut.
+ *   ROW_TILES: a workgroup owns 128 query rows of one (sequence, kv head) and
+ *     shares every K/V tile among them; every mask kind, the valid-slot list,
+ *     register or shadow staging, split-K.
+ *   KEY_SPLIT: a workgroup owns 32 query rows and all their keys; its four
+ *     waves split the keys and merge their partials in the kernel (no split-K
+ *     workspace, no second launch).  FULL mask, f16 V shadow given, no
+ *     valid-slot list, head_dim 128 or 256, splits 0 or 1, p_bf16 off;
+ *     anything else returns EMB_ERR_UNSUPPORTED.  For few rows per kv head
+ *     (the pi0.5 / GR00T / HY-VLA action experts: 51 tokens x 8 q-heads).
+ *   AUTO: KEY_SPLIT where it applies and max_q * (hq / hkv) <= 512, else
+ *     ROW_TILES.
+ * The two kernels add the same terms in different orders, so their outputs
+ * agree within rounding, not bit for bit. */
+#define EMB_ATTN_AUTO 0
+#define EMB_ATTN_ROW_TILES 1
+#define EMB_ATTN_KEY_SPLIT 2
 
 size_t emb_attn_workspace_bytes(int32_t batch, int32_t max_q, int32_t hq, int32_t hkv,
                                 int32_t head_dim, int32_t splits);

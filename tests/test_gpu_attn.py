@@ -67,10 +67,14 @@ class Seqs:
         self.cu_q = np.concatenate([[0], np.cumsum(n_q)]).astype(np.int32)
 
     def run(self, emb, torch, dev, scale, splits=1, uniform=False, **kw):
-        """Runs the attention twice -- tiles staged through registers from the bf16
-        V pool, and copied into LDS from the f16 V shadow -- and requires the two
-        to agree bit for bit (same arithmetic, same conversions).  uniform: the
-        batch goes in the form without bounds arrays (equal sequences only)."""
+        """Runs the row-tile kernel twice -- tiles staged through registers from the
+        bf16 V pool, and copied into LDS from the f16 V shadow -- and requires the
+        two to agree bit for bit (same arithmetic, same conversions).  Where the
+        key-split kernel applies (FULL mask, no split-K, D 128/256) it runs too:
+        its output is kept in ks_out (the callers check it against the oracle
+        with ks_check) and must agree with the row-tile output within the bar.
+        uniform: the batch goes in the form without bounds arrays (equal
+        sequences only)."""
         if uniform:
             assert len(set(self.n_keys)) == 1 and len(set(self.n_q)) == 1
         ws = None
@@ -81,8 +85,7 @@ class Seqs:
                     vp=_t(torch, dev, self.vp), v16=_t(torch, dev, v16_shadow(self.vp, self.d)),
                     bt=_t(torch, dev, self.bt), cu=_t(torch, dev, self.cu_q),
                     nk=_t(torch, dev, np.array(self.n_keys, np.int32)))
-        outs = []
-        for v16 in (None, keep["v16"]):
+        def launch(v16, kernel):
             out = torch.full((int(self.cu_q[-1]), self.hq, self.d), float("nan"), dtype=torch.float32, device=dev)
             emb.paged_attention(q=keep["q"], out=out, k_pool=keep["kp"], v_pool=keep["vp"], v16_pool=v16,
                                 batch=len(self.n_q), hq=self.hq, hkv=self.hkv, d=self.d, max_q=max(self.n_q),
@@ -90,13 +93,35 @@ class Seqs:
                                 n_keys=None if uniform else keep["nk"],
                                 n_keys_uniform=self.n_keys[0] if uniform else 0,
                                 block_tables=keep["bt"], bt_stride=self.bt_stride, splits=splits, workspace=ws,
-                                **kw)
+                                kernel=kernel, **kw)
             torch.cuda.synchronize()
-            outs.append(out.cpu().numpy())
+            return out.cpu().numpy()
+
+        outs = [launch(None, emb.EMB_ATTN_ROW_TILES), launch(keep["v16"], emb.EMB_ATTN_ROW_TILES)]
         assert np.array_equal(outs[0], outs[1], equal_nan=True), "register and LDS-copy paths differ"
-        self.reg_out = [outs[0][self.cu_q[b]:self.cu_q[b + 1]] for b in range(len(self.n_q))]
-        o = outs[1]
-        return [o[self.cu_q[b]:self.cu_q[b + 1]] for b in range(len(self.n_q))]
+        per_seq = lambda o: [o[self.cu_q[b]:self.cu_q[b + 1]] for b in range(len(self.n_q))]
+        self.reg_out = per_seq(outs[0])
+        self.ks_out = None
+        if (splits <= 1 and kw.get("mask_kind", emb.EMB_MASK_FULL) == emb.EMB_MASK_FULL and self.d in (128, 256)
+                and not kw.get("p_bf16") and kw.get("valid_slots") is None):
+            ks = launch(keep["v16"], emb.EMB_ATTN_KEY_SPLIT)
+            for b in range(len(self.n_q)):
+                sl = slice(self.cu_q[b], self.cu_q[b + 1])
+                mag = max(float(np.abs(outs[1][sl]).max(initial=0.0)), 1e-30)  # the bar relative to the data's scale
+                assert_close(ks[sl] / mag, outs[1][sl] / mag, f"key-split vs row tiles, seq {b}")
+            self.ks_out = per_seq(ks)
+        return per_seq(outs[1])
+
+    def ks_check(self, orc, scale, what, rows=None, **kw):
+        """The key-split output of the last run against the oracle (all rows, or
+        the given rows of every sequence); the last run must have run it."""
+        assert self.ks_out is not None, f"{what}: the key-split kernel did not run"
+        for b in range(len(self.n_q)):
+            ref = self.oracle(orc, b, scale, rows=rows, **kw)
+            got = self.ks_out[b]
+            if rows is not None:
+                got, ref = got[rows], ref[rows]
+            assert_close(got, ref, f"{what} key-split seq {b}")
 
     def oracle(self, orc, b, scale, rows=None, **kw):
         return orc.gqa_attention(self.q[b], self.k[b], self.v[b], self.n_q[b], self.n_keys[b], self.hq, self.hkv,
@@ -111,6 +136,7 @@ def test_pi05_action_expert_shape(emb, orc, torch_dev):
     scale = 1 / 16
     got = s.run(emb, torch, dev, scale)[0]
     assert_close(got, s.oracle(orc, 0, scale), "pi05 cfg1")
+    s.ks_check(orc, scale, "pi05 cfg1")
     got4 = s.run(emb, torch, dev, scale, splits=4)[0]
     assert_close(got4, s.oracle(orc, 0, scale), "pi05 cfg1 split-K 4")
     got6 = s.run(emb, torch, dev, scale, splits=6)[0]
@@ -131,6 +157,8 @@ def test_pi05_register_path_against_oracle(emb, orc, torch_dev):
             ref = s.oracle(orc, b, scale)
             assert_close(got[b], ref, f"shadow path b={b} splits={splits}")
             assert_close(s.reg_out[b], ref, f"register path b={b} splits={splits}")
+        if splits == 1:
+            s.ks_check(orc, scale, "pi05 two sequences")
 
 
 def test_uniform_batch_form(emb, orc, torch_dev):
@@ -145,6 +173,8 @@ def test_uniform_batch_form(emb, orc, torch_dev):
         for b in range(3):
             assert np.array_equal(arr[b], uni[b]), f"uniform form differs, splits {splits} seq {b}"
             assert_close(uni[b], s.oracle(orc, b, 1 / 16), f"uniform seq {b} splits {splits}")
+        if splits == 1:
+            s.ks_check(orc, 1 / 16, "uniform form")
 
 
 @pytest.mark.parametrize("d,hq,hkv", [(256, 8, 1), (128, 4, 2), (64, 2, 2)])
@@ -228,6 +258,9 @@ def test_multi_session_sweep(emb, orc, torch_dev, B, splits, split_keys):
             assert_close(got[b], ref, f"B={B} session {b}")
         else:
             assert_close(got[b][rows], ref[rows], f"B={B} session {b} rows {rows.tolist()}")
+        if s.ks_out is not None:
+            ks = s.ks_out[b] if rows is None else s.ks_out[b][rows]
+            assert_close(ks, ref if rows is None else ref[rows], f"B={B} session {b} key-split")
 
 
 def test_split_keys_uniform_batch(emb, orc, torch_dev):
@@ -253,6 +286,7 @@ def test_prefill_prefix_lm_rows(emb, orc, torch_dev):
     rows = np.concatenate([np.arange(0, 20), np.arange(400, 420), np.arange(796, 816)])
     ref = s.oracle(orc, 0, 1 / 16, rows=rows)
     assert_close(got[rows], ref[rows], "prefill rows")
+    assert_close(s.ks_out[0][rows], ref[rows], "prefill rows key-split")
 
 
 def test_lingbot_chunk_step_rows(emb, orc, torch_dev):
@@ -264,6 +298,7 @@ def test_lingbot_chunk_step_rows(emb, orc, torch_dev):
     rows = np.array([0, 1, 31, 32, 777, 1023, 1500, 1559])
     ref = s.oracle(orc, 0, 1 / math.sqrt(128), rows=rows)
     assert_close(got[rows], ref[rows], "lingbot rows")
+    assert_close(s.ks_out[0][rows], ref[rows], "lingbot rows key-split (878 pages: table entries past 128)")
 
 
 @pytest.mark.parametrize("window", [-1, 1])
@@ -402,6 +437,8 @@ def test_head_dims_and_ragged_batch(emb, orc, torch_dev, d):
     got = s.run(emb, torch, dev, 1 / math.sqrt(d))
     for b in range(len(nq)):
         assert_close(got[b], s.oracle(orc, b, 1 / math.sqrt(d)), f"d={d} b={b}")
+    if d >= 128:
+        s.ks_check(orc, 1 / math.sqrt(d), f"d={d}")
     got3 = s.run(emb, torch, dev, 1 / math.sqrt(d), splits=3)
     for b in range(len(nq)):
         assert_close(got3[b], s.oracle(orc, b, 1 / math.sqrt(d)), f"d={d} b={b} split 3")

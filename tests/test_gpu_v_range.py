@@ -57,6 +57,8 @@ def test_paged_paths_any_v_range(emb, orc, torch_dev, d, hq, hkv, name, vs):
             ref = s.oracle(orc, b, sc)
             assert np.all(np.isfinite(got[b])), f"{name} d={d} splits={splits} b={b}: non-finite"
             assert_close(got[b] / vs, ref / vs, f"{name} d={d} splits={splits} b={b}")
+            if s.ks_out is not None:
+                assert_close(s.ks_out[b] / vs, ref / vs, f"{name} d={d} b={b} key-split")
 
 
 def test_mixed_page_magnitudes(emb, orc, torch_dev):
@@ -74,6 +76,8 @@ def test_mixed_page_magnitudes(emb, orc, torch_dev):
     for splits in (1, 3):
         got = s.run(emb, torch, dev, 1 / 16, splits=splits)[0]
         _close_rows(got, s.oracle(orc, 0, 1 / 16), f"mixed splits={splits}")
+        if splits == 1:
+            _close_rows(s.ks_out[0], s.oracle(orc, 0, 1 / 16), "mixed key-split")
 
 
 @pytest.mark.parametrize("name,vs", SCALES)
