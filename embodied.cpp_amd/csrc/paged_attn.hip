@@ -1597,7 +1597,17 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
         return EMB_OK;
     }
     const int64_t rows_per_unit = (int64_t)a->max_q * kp.G;
-    if (ks_ok && (a->kernel == EMB_ATTN_KEY_SPLIT || (a->kernel == EMB_ATTN_AUTO && rows_per_unit <= 512))) {
+    // Automatic choice: the key-split kernel reads every K/V tile once per 32
+    // rows instead of once per 128, so it pays off only while the row tiles
+    // would leave most of the GPU idle (at most half the CUs busy unsplit).
+    bool ks_auto = false;
+    if (ks_ok && a->kernel == EMB_ATTN_AUTO && rows_per_unit <= 512) {
+        int dev = 0, n_cu = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+            ks_auto = 2 * (int64_t)a->batch * a->hkv * kp.row_tiles <= n_cu;
+    }
+    if (ks_ok && (a->kernel == EMB_ATTN_KEY_SPLIT || ks_auto)) {
         KsParams ks{};
         ks.q = kp.q;
         ks.out = kp.out;

@@ -17,13 +17,20 @@
 // a workgroup owns one 32-row block and ALL its keys, and its four waves split
 // the keys among themselves:
 //   * wave w takes key tiles w, w+4, w+8, ... (32 keys each);
-//   * each wave loads its tiles' K rows and f16 V-shadow chunks from global
-//     memory straight into the MFMA operand registers -- no LDS and no
-//     barrier inside the key loop; the four waves of a CU run independently;
+//   * each wave stages its own tiles: K rows are copied into two LDS stages
+//     of the wave (buffer loads that write LDS, whole rows, 1 KB a copy), the
+//     f16 V-shadow chunks are loaded straight into the P.V operand registers;
+//     no barrier inside the key loop, the four waves of a CU run
+//     independently;
 //   * the four partial (O, m, l) merge through LDS at the end and the
 //     workgroup writes its 32 output rows once.
 // 18 x 13 = 234 workgroups for the pi0.5 step: no merge launch, no partials
-// in HBM, 416 rows computed for 408 (the row-tile kernel computes 512).
+// in HBM, 416 rows computed for 408 (the row-tile kernel computes 512).  The
+// price: every CU streams a whole layer's K/V (888 KB at pi0.5 shape), 3.25x
+// the row tiles' L2 -> CU traffic.  Measured on MI355X, one CU streams at most
+// 70-90 GB/s and the L2s together 10-15 TB/s, so the key loop takes about as
+// long as the streaming alone; the kernel wins while the row tiles would
+// leave most CUs idle (the host's automatic choice, emb_kv.h).
 //
 // Per wave and key tile the MFMA math is the row-tile kernel's, transposed:
 //   S^T[32 keys x 32 rows] = K . Q^T   (bf16 32x32x16, f32 accumulation)
@@ -31,24 +38,28 @@
 // lane l owns query row l%32; the 16 scores a lane holds for a tile are keys
 // (r/4)*8 + (l/32)*4 + r%4 (r = 0..15), so the row max is one lane swap.
 //
-// Operand registers straight from memory:
-//   K: lane l reads 16 bytes of key row (tile*32 + l%32), dims kk*16 +
-//      (l/32)*8 + [0,8), for kk = 0..D/16-1 -- exactly the A operand.
+// Operands:
+//   K: fragment kk of the S product is row l%32, 16-byte chunk kk*2 + l/32
+//      of the LDS stage (chunks XOR-swizzled by row: conflict-free reads).
 //   V: the f16 shadow page holds each dim's 16 keys in the order the P.V
 //      MFMA consumes them (emb_common.h v16_index), so the A operand of page
 //      kp, dims dt*32 + [0,32), is one 16-byte read a lane: 1 KB contiguous
 //      per instruction.
-// A missing key (past the limit, unmapped page) reads from a zero block
-// instead, so a load never needs a branch or a bounds check; keys past
-// n_keys are masked (score -inf) and their V read as zeros on the last tile.
+// Missing keys (past the limit, unmapped pages): K copies through a
+// descriptor that ends at the page's last valid row read zeros; V reads from
+// a zero block, and V of keys past the limit inside the last page is masked
+// to zero; keys past n_keys are masked (score -inf).
 //
 // Pipeline per wave: while the S MFMAs of tile i+1 run, the softmax VALU work
 // of tile i is interleaved between them; while the P.V MFMAs of tile i run,
-// the mask and row max of tile i+1 are.  K of tile i+2 is loaded as soon as
-// the S MFMAs of tile i+1 have read their registers, V of tile i+1 as soon as
-// the P.V MFMAs of tile i have.  The online softmax is the row-tile kernel's:
-// running max in raw score units, accumulators rescaled only when a row's max
-// grows by more than 2^8 (a wave-uniform branch most tiles skip).
+// the mask and row max of tile i+1, the V loads of tile i+1 (each into the
+// register its MFMA has just read) and the K copies of tile i+3 are.  K is
+// two tiles ahead, V one.  Past the wave's last tile the loads read zeros
+// and one extra S is computed and dropped: measured, this branch-free form
+// is faster than a peeled last tile (25.9 vs 26.8 us at config 1).  The
+// online softmax is the row-tile kernel's: running max in raw score units,
+// accumulators rescaled only when a row's max grows by more than 2^8 (a
+// wave-uniform branch most tiles skip).
 //
 // Exactness: as in the row-tile kernel, a workgroup any of whose waves ended
 // with a non-finite partial, or a partial whose largest |O| is below 2^-12
@@ -141,7 +152,8 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
             ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
             (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a));
     };
-    // Source of this lane's K operand for tile t: key t*32 + lrow, dims lhi*8 + kk*16.
+    // Exact path: source of this lane's K operand for tile t (key t*32 + lrow,
+    // dims lhi*8 + kk*16), read straight into registers.
     auto k_src = [&](int32_t t, int32_t pid0, int32_t pid1) -> const uint16_t * {
         const int32_t key = t * 32 + lrow;
         const int32_t pid = lrow < 16 ? pid0 : pid1;

@@ -428,11 +428,15 @@ typedef struct emb_attn_args {
  *   KEY_SPLIT: a workgroup owns 32 query rows and all their keys; its four
  *     waves split the keys and merge their partials in the kernel (no split-K
  *     workspace, no second launch).  FULL mask, f16 V shadow given, no
- *     valid-slot list, head_dim 128 or 256, splits 0 or 1, p_bf16 off;
- *     anything else returns EMB_ERR_UNSUPPORTED.  For few rows per kv head
- *     (the pi0.5 / GR00T / HY-VLA action experts: 51 tokens x 8 q-heads).
- *   AUTO: KEY_SPLIT where it applies and max_q * (hq / hkv) <= 512, else
- *     ROW_TILES.
+ *     valid-slot list, head_dim 128 or 256, splits 0 or 1, p_bf16 off,
+ *     bt_stride <= 2048 (tables of up to 32768 keys); anything else returns
+ *     EMB_ERR_UNSUPPORTED.  For few rows per kv head (the pi0.5 / GR00T /
+ *     HY-VLA action experts: 51 tokens x 8 q-heads) over few sequences: it
+ *     reads each K/V tile once per 32 rows (the row tiles once per 128), so
+ *     it wins only while the row tiles would leave the GPU mostly idle.
+ *   AUTO: KEY_SPLIT where it applies, max_q * (hq / hkv) <= 512 and the
+ *     unsplit row tiles (batch * hkv * ceil(max_q * hq / hkv / 128)) would
+ *     occupy at most half the device's compute units; else ROW_TILES.
  * The two kernels add the same terms in different orders, so their outputs
  * agree within rounding, not bit for bit. */
 #define EMB_ATTN_AUTO 0
