@@ -375,8 +375,11 @@ def bench_cfg4(c: Ctx, steps, warmup):
         best = None
         sweep = {}
         ks = c.emb.EMB_ATTN_KEY_SPLIT
+        # (2, 640..896): only the long sessions split in two, the short ones
+        # written by their own workgroups (no partials, skipped by the merge)
         for sp, sk, kern in ((1, 0, ks), (1, 0, None), (2, 0, None), (4, 0, None), (8, 0, None), (3, 384, None),
-                             (4, 256, None), (4, 320, None), (6, 192, None), (8, 128, None)):
+                             (4, 256, None), (4, 320, None), (6, 192, None), (8, 128, None), (2, 640, None),
+                             (2, 768, None), (2, 896, None)):
             if B >= 32 and sk == 0 and sp > 2:
                 continue
             P.set_splits(sp, sk, kernel=kern)

@@ -585,8 +585,12 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
         if (p.window >= 0) k_lo = max(0, (qp_min / p.chunk - p.window) * p.chunk);
     }
     int32_t t_lo = k_lo / G::KT, t_hi = (max(k_hi, k_lo) + G::KT - 1) / G::KT;
+    // splits of this sequence: with one (a short sequence of a ragged batch
+    // under split_keys) the workgroup writes its output rows itself, and the
+    // merge kernel skips the sequence
+    const int32_t ns_seq = p.splits > 1 ? seq_splits(p, nk) : 1;
     if (p.splits > 1) {
-        const int32_t ns = seq_splits(p, nk);
+        const int32_t ns = ns_seq;
         if (split >= ns) return;  // a short sequence of a ragged batch: fewer splits (uniform per workgroup)
         const int32_t nt = t_hi - t_lo;
         const int32_t per = (nt + ns - 1) / ns;
@@ -1051,7 +1055,7 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
     // wave stores its 32-row block in the accumulator order: every store
     // instruction writes 512 contiguous bytes, with no staging through LDS.
     // (Rows past the end carry values nothing reads.)
-    if (p.splits > 1) {
+    if (ns_seq > 1) {
         const int64_t unit_row0 = ((int64_t)(b * p.hkv + kvh) * p.splits + split) * ((int64_t)p.row_tiles * ROWS_PER_WG);
         float omax = 0.0f;
 #pragma unroll
@@ -1187,6 +1191,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
         const int64_t rows_per_unit = (int64_t)blocks_per_unit * 32;
         const int64_t unit0 = (int64_t)(b * p.hkv + kvh) * p.splits;
         const int32_t ns = seq_splits(p, p.n_keys ? p.n_keys[b] : p.nk_single);
+        if (ns <= 1) continue;  // one split: the attention kernel wrote the rows itself
         float ms[MS], ls[MS];
         int ks[MS];
         u32x2 os[MS][NCH];

@@ -415,7 +415,9 @@ typedef struct emb_attn_args {
                                           splits; > 0 = a sequence of n keys takes
                                           min(splits, ceil(n / split_keys)) (at least 1), so
                                           short sequences of a ragged batch are not cut into
-                                          splits that cost more than they save */
+                                          splits that cost more than they save; a sequence
+                                          left with one split writes its output directly
+                                          (no partials, no merge work) */
     int32_t kernel;                    /* EMB_ATTN_AUTO (0), EMB_ATTN_ROW_TILES (1) or
                                           EMB_ATTN_KEY_SPLIT (2), below */
 } emb_attn_args;

@@ -236,7 +236,8 @@ def test_null_block_tables_are_identity(emb, orc, torch_dev, d, hq, hkv, mask):
 
 
 @pytest.mark.parametrize("B,splits,split_keys", [(1, 8, 0), (8, 8, 0), (32, 2, 0), (64, 1, 0), (64, 2, 0),
-                                                   (8, 8, 128), (32, 4, 384), (64, 4, 320), (64, 3, 512)])
+                                                   (8, 8, 128), (32, 4, 384), (64, 4, 320), (64, 3, 512),
+                                                   (32, 2, 640), (64, 2, 768)])
 def test_multi_session_sweep(emb, orc, torch_dev, B, splits, split_keys):
     """cfg4 at every batch the bench times, with its prefix lengths and split
     choices: session b's prefix is 300 + x_b % 901, x_b the b-th output of
@@ -244,7 +245,10 @@ def test_multi_session_sweep(emb, orc, torch_dev, B, splits, split_keys):
     pages scattered in one pool.  All rows of every session at B <= 8; 24
     sampled rows of every session at B = 32 and 64.  split_keys > 0: each
     session takes min(splits, ceil(keys / split_keys)) splits, so sessions of
-    one batch are cut differently and the merge reads a count per session."""
+    one batch are cut differently and the merge reads a count per session;
+    a session with one split is written by its own workgroups (no partials)
+    and skipped by the merge (split_keys 640 / 768 leave about half the
+    sessions unsplit)."""
     torch, dev = torch_dev
     lens = [300 + orc.lib().orc_mt64_nth(0xE3BD0004, b + 1) % 901 for b in range(B)]
     assert 300 <= min(lens) and max(lens) <= 1200
