@@ -1582,11 +1582,13 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     EMB_CHECK_ARG(a->kernel >= EMB_ATTN_AUTO && a->kernel <= EMB_ATTN_KEY_SPLIT, "unknown kernel choice");
     const bool ks_ok = a->mask_kind == EMB_MASK_FULL && a->v16_pool && !a->valid_slots && !a->p_bf16 &&
                        (a->head_dim == 128 || a->head_dim == 256) && splits == 1 &&
-                       (!a->block_tables || a->bt_stride <= KS_MAX_PAGES);
+                       (!a->block_tables || a->bt_stride <= KS_MAX_PAGES) &&
+                       (int64_t)a->max_q * a->q_stride * esz < ((int64_t)1 << 31);  // 32-bit query offsets
     if (a->kernel == EMB_ATTN_KEY_SPLIT && !ks_ok)
         return emb::set_error(EMB_ERR_UNSUPPORTED,
                               "the key-split kernel takes the FULL mask, an f16 V shadow, no valid-slot list, "
-                              "head_dim 128 or 256, no split-K, no p_bf16 and at most %d block-table entries",
+                              "head_dim 128 or 256, no split-K, no p_bf16, at most %d block-table entries "
+                              "and a query block under 2 GiB",
                               KS_MAX_PAGES);
     if (a->p_bf16) {
         EMB_CHECK_ARG(splits == 1, "p_bf16 runs unsplit (splits must be 0 or 1)");

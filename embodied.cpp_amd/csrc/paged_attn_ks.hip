@@ -100,6 +100,13 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
     __shared__ __attribute__((aligned(16))) uint16_t ks_k1[KS_WAVES][32 * D];
     __shared__ float mlb[KS_WAVES][32][2];
     __shared__ int32_t tbl[KS_MAX_PAGES];  // the sequence's block-table row
+    // At head_dim 256 with bf16 Q the workgroup's 32 query rows are copied
+    // into LDS once (1 KB copies of two whole rows, the K image's swizzle) and
+    // every wave reads its fragments from there: one 16 KB stream instead of
+    // four waves each loading the rows in 32-byte pieces.  (At head_dim 128
+    // the buffer would cost the second workgroup per CU its LDS.)
+    constexpr bool QLDS = D == 256 && !QF32;
+    __shared__ __attribute__((aligned(16))) uint16_t ks_q[QLDS ? 32 * D : 8];
 
     const int nwg = (int)gridDim.x;
     // XCD-aware order: hardware ids go round-robin over the 8 XCDs; logical ids
@@ -300,10 +307,34 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
 
         const int32_t t0 = wave;
         u32x4 vb[NV];
-        load_q();  // in flight while the table is read
-        if (bt_b) {
+        if constexpr (QLDS) {
+            // copy j (wave w issues j = w, w+4, ...): rows 2j, 2j+1 of the
+            // block; rows past the sequence's queries fall outside the
+            // descriptor and land as zeros
+            const u32x4 qd = buf_desc(reinterpret_cast<const uint16_t *>(p.q) + (int64_t)q_begin * p.q_stride,
+                                      (uint32_t)((int64_t)nq * p.q_stride * 2));
+            asm volatile("s_nop 4");  // VALU-written descriptor SGPRs read by VMEM
+            const uint32_t qlds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t *)ks_q;
+#pragma unroll
+            for (int j = wave; j < 16; j += 4) {
+                const int r = 2 * j + lhi;
+                const int32_t row = row0 + r;
+                const int32_t tk = row / p.G, hd = kvh * p.G + row % p.G;
+                const int c = lrow ^ (r & 15);
+                lds_copy16(qd, qlds + j * 1024, (uint32_t)(((int64_t)tk * p.q_stride + (int64_t)hd * D + c * 8) * 2));
+            }
+        } else {
+            load_q();  // in flight while the table is read
+        }
+        if (bt_b)
             for (int i = threadIdx.x; i < p.bt_stride; i += 256) tbl[i] = bt_b[i];
-            __syncthreads();
+        if constexpr (QLDS) wait_vmcnt<0>();  // the query copies (and the table loads) have landed
+        if (QLDS || bt_b) __syncthreads();
+        if constexpr (QLDS) {
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+                qf[kk] = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const u32x4 *>(&ks_q[lrow * D + (((kk * 2 + lhi) ^ (lrow & 15)) << 3)]));
         }
         {
             const int32_t a0 = page_id(2 * t0), a1 = page_id(2 * t0 + 1);
