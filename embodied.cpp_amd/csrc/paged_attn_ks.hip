@@ -151,6 +151,21 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
         const int32_t id = tbl[min(pi, KS_MAX_PAGES - 1)];  // read unconditionally, then selected (no branch)
         return __builtin_amdgcn_readfirstlane(pi < p.bt_stride ? id : -1);
     };
+    // Page ids of key tile t's two pages (2t, 2t+1) and of tile u's, as one
+    // 8-byte LDS read each and a single wait: straight-line code, so the
+    // reads of both tiles are in flight together.
+    const bool has_bt = bt_b != nullptr;
+    auto page_ids2 = [&](int32_t t, int32_t u, int32_t &t0id, int32_t &t1id, int32_t &u0id, int32_t &u1id) {
+        const i32x2 wt = *reinterpret_cast<const i32x2 *>(&tbl[min(2 * t, KS_MAX_PAGES - 2)]);
+        const i32x2 wu = *reinterpret_cast<const i32x2 *>(&tbl[min(2 * u, KS_MAX_PAGES - 2)]);
+        auto pick = [&](int32_t pi, int32_t id) {
+            return __builtin_amdgcn_readfirstlane(has_bt ? (pi < p.bt_stride ? id : -1) : pi);
+        };
+        t0id = pick(2 * t, wt[0]);
+        t1id = pick(2 * t + 1, wt[1]);
+        u0id = pick(2 * u, wu[0]);
+        u1id = pick(2 * u + 1, wu[1]);
+    };
     // Uniform 64-bit address, its halves forced into SGPRs, as a global
     // (address space 1) pointer, so loads through it are global loads.
     auto uniform_ptr = [](const void *q) {
@@ -337,12 +352,13 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
                     bf16x8, *reinterpret_cast<const u32x4 *>(&ks_q[lrow * D + (((kk * 2 + lhi) ^ (lrow & 15)) << 3)]));
         }
         {
-            const int32_t a0 = page_id(2 * t0), a1 = page_id(2 * t0 + 1);
+            const int32_t t1 = t0 + 4;
+            int32_t a0, a1, b0, b1;
+            page_ids2(t0, t1, a0, a1, b0, b1);
             const KDesc ka = k_desc(t0, a0, a1);
 #pragma unroll
             for (int j = 0; j < NKC; ++j) k_copy(kst0, ka, j);
-            const int32_t b0 = page_id(2 * t0 + 8), b1 = page_id(2 * t0 + 9);
-            const KDesc kb = k_desc(t0 + 4, b0, b1);
+            const KDesc kb = k_desc(t1, b0, b1);
 #pragma unroll
             for (int j = 0; j < NKC; ++j) k_copy(kst1, kb, j);
             load_v(vb, v_src(t0, 0, a0), v_src(t0, 1, a1));
@@ -361,8 +377,9 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
         wait_vmcnt<NKC + NV>();
         f32x16 s_cur = qk_lds(kst0);
         {  // K of tile t0+8 into stage 0, which S of tile t0 has read
-            const int32_t c0 = page_id(2 * t0 + 16), c1 = page_id(2 * t0 + 17);
-            const KDesc kc = k_desc(t0 + 8, c0, c1);
+            const int32_t t2 = t0 + 8;
+            const int32_t c0 = page_id(2 * t2), c1 = page_id(2 * t2 + 1);
+            const KDesc kc = k_desc(t2, c0, c1);
 #pragma unroll
             for (int j = 0; j < NKC; ++j) k_copy(kst0, kc, j);
         }
@@ -381,7 +398,13 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
         // tile has no branch but the (rare) rescale: masks and zeroing are
         // selects, so no register is copied at a merge while a load into it
         // is in flight.
-        auto tile = [&](int32_t t, uint16_t *kn) {
+        // The zero block's address, opaque to the compiler so that it stays in
+        // two SGPRs: otherwise it is reloaded from the GOT on every tile, a
+        // scalar load and a wait in the middle of the loop.
+        uint64_t zero_addr = reinterpret_cast<uint64_t>(ks_zero);
+        asm volatile("" : "+s"(zero_addr));
+        const uint16_t *zero_blk = reinterpret_cast<const uint16_t *>(zero_addr);
+        auto tile = [&](int32_t t, int32_t tn, int32_t tc, uint16_t *kn) {
             // K of tile t+4 has landed: after its last copy (at the end of the
             // P.V phase two tiles back) the previous tile issued NV V loads and
             // NKC copies
@@ -389,6 +412,9 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
             u32x4 kbuf[KAHEAD];
 #pragma unroll
             for (int i = 0; i < KAHEAD; ++i) kbuf[i] = read_k(kn, i);
+            // page ids of tile tn (its V, loaded below) and tile tc (its K copies)
+            int32_t n0, n1, c0, c1;
+            page_ids2(tn, tc, n0, n1, c0, c1);
             if (__builtin_amdgcn_ballot_w64(mt_cur > m_run + p.th_raw) != 0) {
                 const float m_new = fmaxf(m_run, mt_cur);
                 const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
@@ -433,18 +459,16 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
                     const int o0 = kp * 16 + (e0 >> 2) * 8 + (e0 & 3), o1 = kp * 16 + (e1 >> 2) * 8 + (e1 & 3);
                     keep[kp][w] = (o0 < vrel ? 0x0000ffffu : 0u) | (o1 < vrel ? 0xffff0000u : 0u);
                 }
-            const int32_t n0 = page_id(2 * t + 8), n1 = page_id(2 * t + 9);
-            const int32_t c0 = page_id(2 * t + 24), c1 = page_id(2 * t + 25);
-            const KDesc kc = k_desc(t + 12, c0, c1);
-            const gu16 *vs0 = uniform_ptr(t * 32 + 128 < lim && n0 >= 0
+            const KDesc kc = k_desc(tc, c0, c1);
+            const gu16 *vs0 = uniform_ptr(tn * 32 < lim && n0 >= 0
                                                   ? p.v16_pool + ((int64_t)n0 * p.hkv + kvh) * (16 * D)
-                                                  : ks_zero) + vlane;
-            const gu16 *vs1 = uniform_ptr(t * 32 + 144 < lim && n1 >= 0
+                                                  : zero_blk) + vlane;
+            const gu16 *vs1 = uniform_ptr(tn * 32 + 16 < lim && n1 >= 0
                                                   ? p.v16_pool + ((int64_t)n1 * p.hkv + kvh) * (16 * D)
-                                                  : ks_zero) + vlane;
+                                                  : zero_blk) + vlane;
             // keys at or past nk do not exist: score -inf (selects; all kept
             // on every tile but the last)
-            const int32_t srel = nk - (t + 4) * 32 - lhi * 4;
+            const int32_t srel = nk - tn * 32 - lhi * 4;
             float mt_nxt = -INFINITY;
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -475,7 +499,7 @@ __global__ __launch_bounds__(256, D >= 256 ? 1 : 2) void attn_ks_kernel(KsParams
         // the V registers stay the same registers across the back edge (an
         // unrolled pair of tiles let the allocator rename them, and the copies
         // at the back edge waited for loads still in flight).
-        for (int32_t t = t0, i = 0; t < nt; t += 4, ++i) tile(t, (i & 1) ? kst0 : kst1);
+        for (int32_t t = t0, i = 0; t < nt; t += 4, ++i) tile(t, t + 4, t + 12, (i & 1) ? kst0 : kst1);
     }
 
     // every copy into this wave's stages has landed (they become its merge buffer)
