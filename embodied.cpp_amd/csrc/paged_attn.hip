@@ -76,7 +76,7 @@ namespace {
 using namespace emb_attn;
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int WAVES = 4;
+constexpr int WAVES = 4;  // row blocks of a workgroup
 constexpr int ROWS_PER_WAVE = 32;
 constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
 constexpr int SEG_PAGES = 1024;  // block-table entries held in LDS at a time (16384 keys)
@@ -145,7 +145,9 @@ struct KParams {
     // 32-row block in the MFMA accumulator order (element ((c*64 + lane)*4 + e)
     // of a block is dims c*8 + (lane/32)*4 + e of row lane%32)
     uint16_t *ws_o;
-    float *ws_ml;    // [batch*hkv][splits][row_tiles*128][4]: m (log2 units), l, k (O/l stored as O/l * 2^-k), 0
+    // [batch*hkv][splits][row_tiles*128][4]: m (log2 units), l, k0, k1 (dims
+    // [0, D/2) of O/l stored as O/l * 2^-k0, dims [D/2, D) with 2^-k1)
+    float *ws_ml;
 };
 
 // Two bf16 (packed in a dword) -> two f16 (packed in a dword), round to nearest even.
@@ -213,15 +215,16 @@ __device__ __forceinline__ void page_rsrc(const KParams &p, const uint16_t *vbas
 
 
 // DMA path: the tile's K rows and f16 V-shadow pages go straight into the
-// stage.  Wave w copies 1 KB blocks b = 4j + w of each image; block b of the
+// stage.  Wave w of NW copies 1 KB blocks b = NW*j + w of each image; block b of the
 // K image holds key rows [b*64/CH, (b+1)*64/CH), so lane i loads the global
 // chunk that the XOR swizzle puts at slot (b*64 + i) % CH of its row.  A block
 // never crosses a page, so one descriptor serves all 64 lanes.  The per-lane
 // byte offsets do not depend on the tile and are computed once.
-template <int D>
+template <int D, int NW = WAVES>
 struct DmaPlan {
     using G = Geo<D>;
-    static constexpr int NB = G::BLOCKS / 4;  // blocks per wave and image
+    static_assert(G::BLOCKS % NW == 0, "copies must split evenly over the waves");
+    static constexpr int NB = G::BLOCKS / NW;  // blocks per wave and image
     static constexpr int PER_TILE = 2 * NB;   // copies per wave and tile
     static constexpr int RB = 64 / G::CH;     // key rows per K block
     uint32_t koff[NB], voff[NB];
@@ -232,13 +235,13 @@ struct DmaPlan {
         wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const int b = j * 4 + wave;
+            const int b = j * NW + wave;
             const int q = b * 64 + lane;
             const int r = q / G::CH, sl = q % G::CH;
             const int c = sl ^ (r & G::SWZ);
             koff[j] = ((r & 15) * D + c * 8) * 2;
             // V image: page pp covers blocks [pp*D/32, (pp+1)*D/32)
-            const int pp = D >= 128 ? (j * 4 * 32) / D : 2 * j + (wave >> 1);
+            const int pp = D >= 128 ? (j * NW * 32) / D : 2 * j + (wave >> 1);
             voff[j] = b * 1024 - pp * D * 32 + lane * 16;
         }
     }
@@ -278,23 +281,24 @@ struct DmaPlan {
     }
 
     // Copy n of this wave's PER_TILE copies of a tile into the stage at LDS
-    // byte address st: n < NB is K block 4n + w, the rest V blocks.
+    // byte address st: n < NB is K block NW*n + w, the rest V blocks.
     __device__ __forceinline__ void copy(const Descs &ds, uint32_t st, int n) const {
         if (n < NB) {
-            const int j = n, b = j * 4 + wave;
+            const int j = n, b = j * NW + wave;
             u32x4 dk;
-            // page of K block b = (4j + w) * RB / 16: j*RB/4 for RB <= 4 (w < 4),
-            // 2j + w/2 for RB = 8 (D = 64)
-            if constexpr (RB <= 4)
-                dk = ds.kd[(j * RB) / 4];
+            // page of K block b = (NW*j + w) * RB / 16: j*NW*RB/16 while
+            // NW*RB <= 16 (w < NW), 2j + w/2 for RB = 8 (D = 64, NW = 4)
+            static_assert(NW * RB <= 16 || (RB == 8 && NW == 4), "K block page");
+            if constexpr (NW * RB <= 16)
+                dk = ds.kd[(j * NW * RB) / 16];
             else
                 dk = (wave >> 1) ? ds.kd[2 * j + 1] : ds.kd[2 * j];
             lds_copy16(dk, __builtin_amdgcn_readfirstlane(st + b * 1024), koff[j]);
         } else {
-            const int j = n - NB, b = j * 4 + wave;
+            const int j = n - NB, b = j * NW + wave;
             u32x4 dv;
             if constexpr (D >= 128)
-                dv = ds.vd[(j * 4 * 32) / D];
+                dv = ds.vd[(j * NW * 32) / D];
             else
                 dv = (wave >> 1) ? ds.vd[2 * j + 1] : ds.vd[2 * j];
             lds_copy16(dv, __builtin_amdgcn_readfirstlane(st + G::K_ELEMS * 2 + b * 1024), voff[j]);
@@ -451,10 +455,12 @@ struct RegLoader {
     }
 };
 
-// pt[i] = page id of page index seg_p0 + i, or -1 at and past p_end.
-// (All loads first, then all LDS writes: one memory round trip, not four.)
+// pt[i] = page id of page index seg_p0 + i, or -1 at and past p_end, written
+// by the first 256 threads.  (All loads first, then all LDS writes: one
+// memory round trip, not four.)
 __device__ __forceinline__ void load_segment(const int32_t *bt_b, int32_t seg_p0, int32_t p_end, int32_t *pt) {
-    static_assert(SEG_PAGES % 256 == 0, "segment must split evenly over the workgroup");
+    static_assert(SEG_PAGES % 256 == 0, "segment must split evenly over 256 threads");
+    if (threadIdx.x >= 256) return;
     int32_t v[SEG_PAGES / 256];
 #pragma unroll
     for (int k = 0; k < SEG_PAGES / 256; ++k) {
@@ -470,18 +476,27 @@ __device__ __forceinline__ void load_segment(const int32_t *bt_b, int32_t seg_p0
 // values that do not fit live outside the key loop): a third wave per SIMD
 // hides more of each tile's latency.  The masked and register-staged
 // variants would spill inside the loop there, so they keep two.
-template <int D, int MASK, int LD>
+template <int D, int MASK, int LD, int NW = WAVES>
 constexpr int wg_per_cu() {
+    if constexpr (NW > WAVES) return 1;
     return D == 128 && LD == LD_DMA && MASK == EMB_MASK_FULL ? 3 : Geo<D>::MIN_WG;
 }
 
-template <int D, int MASK, int LD, bool QF32>
-__global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_kernel(KParams p) {
+// NW = 4: wave w owns row block w and all D output dims.  NW = 8 (head_dim
+// 256, DMA staging): wave w owns row block w % 4 and half w / 4 of the output
+// dims; both halves of a row block compute the same scores and softmax (so
+// they agree bit for bit on the running max and sum), each its own half of
+// P.V.  Half the accumulators and the query in AGPRs fit a wave into 256
+// registers: two waves per SIMD instead of one, each with half the P.V work.
+template <int D, int MASK, int LD, bool QF32, int NW>
+__global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged_attn_kernel(KParams p) {
     using G = Geo<D>;
     constexpr bool VALID = LD == LD_VALID;
+    static_assert(NW == WAVES || (NW == 2 * WAVES && LD == LD_DMA && D == 256), "eight waves: D 256, DMA staging");
+    constexpr int DW = NW == WAVES ? D : D / 2;  // output dims of a wave
     // four stages when the copies bypass registers (a tile's loads get two
     // iterations to land), three otherwise and where three workgroups share a CU
-    constexpr int NST = LD == LD_DMA && wg_per_cu<D, MASK, LD>() < 3 ? 4 : 3;
+    constexpr int NST = LD == LD_DMA && wg_per_cu<D, MASK, LD, NW>() < 3 ? 4 : 3;
     __shared__ __attribute__((aligned(16))) uint16_t smem[NST * G::STAGE];
     __shared__ __attribute__((aligned(16))) int32_t pt[VALID ? 4 : SEG_PAGES];
 
@@ -512,10 +527,13 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
     const int lane = threadIdx.x & 63;
     const int lrow = lane & 31;
     const int lhi = lane >> 5;
-    const int32_t my_row = row0 + wave * ROWS_PER_WAVE + lrow;
+    const int rbw = __builtin_amdgcn_readfirstlane(wave & (WAVES - 1));  // row block of the wave
+    const int dh = NW == WAVES ? 0 : __builtin_amdgcn_readfirstlane(wave / WAVES);  // its half of the dims
+    const int dt0 = dh * (DW / 32);  // first 32-dim block of O the wave owns
+    const int32_t my_row = row0 + rbw * ROWS_PER_WAVE + lrow;
     const bool row_ok = my_row < rows;
     // a wave past the last row only helps stage tiles (and meets the barriers)
-    const bool wave_live = __builtin_amdgcn_readfirstlane(row0 + wave * ROWS_PER_WAVE) < rows;
+    const bool wave_live = __builtin_amdgcn_readfirstlane(row0 + rbw * ROWS_PER_WAVE) < rows;
     const int32_t tok = row_ok ? my_row / p.G : 0;
     const int32_t head = kvh * p.G + (row_ok ? my_row % p.G : 0);
     const int32_t qpos = qpos0 + tok;
@@ -566,7 +584,9 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
     // arch VGPRs; the read-only query fragment moves to AGPRs, which MFMA reads
     // directly.  (Done once the loads have landed, so the move does not wait.)
     auto pin_q = [&]() {
-        if constexpr (D >= 256) {
+        // (not with eight waves: there every register, accumulators included,
+        // is an arch VGPR -- 256 a wave -- and the query stays among them)
+        if constexpr (D >= 256 && NW == WAVES) {
 #pragma unroll
             for (int kk = 0; kk < D / 16; ++kk) {
                 u32x4 w = __builtin_bit_cast(u32x4, qf[kk]);
@@ -605,9 +625,9 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
         full_lo = p.window >= 0 ? max(0, (qp_max / p.chunk - p.window) * p.chunk) : 0;
     }
 
-    f32x16 acc_o[D / 32];
+    f32x16 acc_o[DW / 32];
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) acc_o[i] = f32x16{};
+    for (int i = 0; i < DW / 32; ++i) acc_o[i] = f32x16{};
     float m_run = -INFINITY, l_run = 0.0f;
 
     const int32_t lim = min(nk, p.capacity);  // slots at or past the capacity are zero rows
@@ -620,7 +640,7 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
     int32_t seg_len = windowed ? WIN_PAGES : SEG_PAGES;
 
     // DMA staging: copies straight into a stage (the lane offsets are fixed).
-    DmaPlan<D> dma;
+    DmaPlan<D, NW> dma;
     if constexpr (LD == LD_DMA) dma.init();
     const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
     // LDS table offset of tile tt's page ids, reloading the next segment when
@@ -787,11 +807,13 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
     // AHEAD steps later, so the MFMAs never wait out the LDS latency, and the
     // copies trickle into the address unit instead of stalling all waves at
     // once at the top of the tile.
-    constexpr int KS = D / 16;                 // k-steps of one 32-key S block
-    constexpr int NS = G::KB * KS;             // S MFMAs a tile
-    constexpr int NPV = G::KB * 2 * (D / 32);  // P.V MFMAs a tile
-    constexpr int EPM = G::KB * 16 / NS;       // score elements per step (both phases)
-    static_assert(NPV * EPM == G::KB * 16 && 2 * DmaPlan<D>::PER_TILE <= NPV, "tile schedule");
+    using DP = DmaPlan<D, NW>;
+    constexpr int KS = D / 16;                  // k-steps of one 32-key S block
+    constexpr int NS = G::KB * KS;              // S MFMAs a tile
+    constexpr int NPV = G::KB * 2 * (DW / 32);  // P.V MFMAs a tile (the wave's dims)
+    constexpr int EPS = G::KB * 16 / NS;        // score elements per S step
+    constexpr int EPV = G::KB * 16 / NPV;       // and per P.V step
+    static_assert(NS * EPS == G::KB * 16 && NPV * EPV == G::KB * 16 && 2 * DP::PER_TILE <= NPV, "tile schedule");
     //
     // The loop runs NST tiles an iteration (tile t_lo + i sits in stage i %
     // NST), so every stage index is a compile-time constant: LDS addresses
@@ -805,7 +827,7 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
         const int nx1 = cur + 1 == NST ? 0 : cur + 1;
         const int nxl = cur == 0 ? NST - 1 : cur - 1;  // receives tile t + NST - 1
         const bool more = t + NST - 1 < t_hi;
-        typename DmaPlan<D>::Descs dsc;
+        typename DP::Descs dsc;
         const uint32_t st_l = smem_lds + nxl * (G::STAGE * 2);
         if constexpr (LD == LD_DMA) {
             // Past the last tile the copies still run, through empty
@@ -825,7 +847,7 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
                 const float m_new = fmaxf(m_run, mt_cur);
                 const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
 #pragma unroll
-                for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
+                for (int i = 0; i < DW / 32; ++i) acc_o[i] *= alpha;
                 l_run *= alpha;
                 m_run = m_new;
             }
@@ -835,9 +857,9 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
             auto read_k = [&](int i) {
                 return *reinterpret_cast<const u32x4 *>(&stk[k_off<D>((i / KS) * 32 + lrow, (i % KS) * 2 + lhi)]);
             };
-            auto read_v = [&](int i) {  // i = (kb*2 + pg) * (D/32) + dt
+            auto read_v = [&](int i) {  // i = (kb*2 + pg) * (DW/32) + dt, dims (dt0 + dt)*32 + [0, 32)
                 return *reinterpret_cast<const u32x4 *>(
-                    &stv[v_off<D>(i / (D / 32), (i % (D / 32)) * 32 + lrow, lhi)]);
+                    &stv[v_off<D>(i / (DW / 32), (dt0 + i % (DW / 32)) * 32 + lrow, lhi)]);
             };
             f32x16 s_nxt[G::KB];
             const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * p.c_log2;
@@ -853,8 +875,8 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
                                                                    kk == 0 ? f32x16{} : s_nxt[kb], 0, 0, 0);
                 if (i + AHEAD < NS) kbuf[i % AHEAD] = read_k(i + AHEAD);
 #pragma unroll
-                for (int u = 0; u < EPM; ++u) {
-                    const int el = i * EPM + u, eb = el / 16, r = el % 16;
+                for (int u = 0; u < EPS; ++u) {
+                    const int el = i * EPS + u, eb = el / 16, r = el % 16;
                     const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[eb][r], p.c_log2, neg_mc));
                     pf[eb][r >> 3][r & 7] = (_Float16)e;
                     // row sum of exactly the f16 weights the P.V product uses
@@ -876,15 +898,15 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < NPV; ++i) {
-                const int kp = i / (D / 32), dt = i % (D / 32);
+                const int kp = i / (DW / 32), dt = i % (DW / 32);
                 acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vbuf[i % AHEAD]),
                                                                   pf[kp >> 1][kp & 1], acc_o[dt], 0, 0, 0);
                 if (i + AHEAD < NPV) vbuf[i % AHEAD] = read_v(i + AHEAD);
                 if constexpr (LD == LD_DMA)
-                    if ((i & 1) && (i >> 1) < DmaPlan<D>::PER_TILE) dma.copy(dsc, st_l, i >> 1);
+                    if ((i & 1) && (i >> 1) < DP::PER_TILE) dma.copy(dsc, st_l, i >> 1);
 #pragma unroll
-                for (int u = 0; u < EPM; ++u) {
-                    const int el = i * EPM + u;
+                for (int u = 0; u < EPV; ++u) {
+                    const int el = i * EPV + u;
                     mt_nxt = fmaxf(mt_nxt, s_nxt[el / 16][el % 16]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -898,14 +920,14 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
             for (int kb = 0; kb < G::KB; ++kb) s_cur[kb] = s_nxt[kb];
         } else if constexpr (LD == LD_DMA) {
 #pragma unroll
-            for (int n = 0; n < DmaPlan<D>::PER_TILE; ++n) dma.copy(dsc, st_l, n);
+            for (int n = 0; n < DP::PER_TILE; ++n) dma.copy(dsc, st_l, n);
         }
         if constexpr (LD == LD_DMA) {
             // tile t+2 (needed by the next S) has landed; with four stages
             // tile t+3, issued this tile, may still fly; after the last tile
             // nothing may (the epilogue reuses the stages)
             if (t + 1 < t_hi)
-                wait_vmcnt<(NST - 3) * DmaPlan<D>::PER_TILE>();
+                wait_vmcnt<(NST - 3) * DP::PER_TILE>();
             else
                 wait_vmcnt<0>();
         } else if (more) {
@@ -934,7 +956,7 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
         float amax = 0.0f;
         bool fin = true;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < DW / 32; ++dt)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 fin = fin && __builtin_isfinite(acc_o[dt][e]);
@@ -950,7 +972,7 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
             load_q();
             pin_q();
 #pragma unroll
-            for (int i = 0; i < D / 32; ++i) acc_o[i] = f32x16{};
+            for (int i = 0; i < DW / 32; ++i) acc_o[i] = f32x16{};
             float m_x = -INFINITY, l_x = 0.0f;
             // logical slot of key j (-1: a zero row), and its page
             auto slot_of = [&](int32_t j) {
@@ -990,7 +1012,7 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
                 const float m_new = fmaxf(m_x, tile_max(sx));
                 const float alpha = m_x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_x - m_new) * p.c_log2);
 #pragma unroll
-                for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
+                for (int i = 0; i < DW / 32; ++i) acc_o[i] *= alpha;
                 l_x *= alpha;
                 m_x = m_new;
                 const float neg = m_new == -INFINITY ? 0.0f : -m_new * p.c_log2;
@@ -1022,8 +1044,8 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
                             vr[m] = page_row(vs[m]);
                         }
 #pragma unroll
-                        for (int dt = 0; dt < D / 32; ++dt) {
-                            const int d = dt * 32 + lrow;
+                        for (int dt = 0; dt < DW / 32; ++dt) {
+                            const int d = (dt0 + dt) * 32 + lrow;
                             u32x4 vw;
 #pragma unroll
                             for (int m = 0; m < 8; m += 2) {
@@ -1057,9 +1079,9 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
     // (Rows past the end carry values nothing reads.)
     if (ns_seq > 1) {
         const int64_t unit_row0 = ((int64_t)(b * p.hkv + kvh) * p.splits + split) * ((int64_t)p.row_tiles * ROWS_PER_WG);
-        float omax = 0.0f;
+        float omax = 0.0f;  // over the wave's dims: with two halves, each has its own scale
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < DW / 32; ++dt)
 #pragma unroll
             for (int e = 0; e < 16; ++e) omax = fmaxf(omax, fabsf(acc_o[dt][e]));
         {
@@ -1072,42 +1094,48 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
         const int k = omax > 0.0f ? min(max(ex - 15, -100), 100) : 0;  // omax * 2^-k in [2^14, 2^15)
         if (row_ok && lhi == 0) {
             const int64_t rowi = unit_row0 + my_row;
-            *reinterpret_cast<f32x4 *>(p.ws_ml + rowi * 4) =
-                f32x4{m_run == -INFINITY ? -INFINITY : m_run * p.c_log2, l_run, (float)k, 0.0f};
+            const float m_out = m_run == -INFINITY ? -INFINITY : m_run * p.c_log2;
+            if constexpr (NW == WAVES) {
+                *reinterpret_cast<f32x4 *>(p.ws_ml + rowi * 4) = f32x4{m_out, l_run, (float)k, (float)k};
+            } else {
+                // (m, l) from the first half (the halves hold the same values), each half's scale
+                if (dh == 0) *reinterpret_cast<f32x2 *>(p.ws_ml + rowi * 4) = f32x2{m_out, l_run};
+                p.ws_ml[rowi * 4 + 2 + dh] = (float)k;
+            }
         }
         if (wave_live) {
             const float scs = ldexpf(sc, -k);
-            uint16_t *blk = p.ws_o + (unit_row0 + row0 + wave * ROWS_PER_WAVE) * D + lane * 4;
+            uint16_t *blk = p.ws_o + (unit_row0 + row0 + rbw * ROWS_PER_WAVE) * D + lane * 4;
 #pragma unroll
-            for (int dt = 0; dt < D / 32; ++dt)
+            for (int dt = 0; dt < DW / 32; ++dt)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const f32x4 v = {acc_o[dt][j * 4] * scs, acc_o[dt][j * 4 + 1] * scs, acc_o[dt][j * 4 + 2] * scs,
                                      acc_o[dt][j * 4 + 3] * scs};
-                    *reinterpret_cast<u32x2 *>(blk + (dt * 4 + j) * 256) = f16x4_bits(v);
+                    *reinterpret_cast<u32x2 *>(blk + ((dt0 + dt) * 4 + j) * 256) = f16x4_bits(v);
                 }
         }
         return;
     }
     // Output rows, the normalised O (f32).  Lane l holds dims dt*32 + j*8 +
-    // (l/32)*4 + [0,4) of row l%32, so a direct 16-byte store touches 64 rows
-    // (cache lines) per instruction.  Where the stages have room, each wave
-    // instead writes its 32 rows x D block into LDS (16-byte chunk c of row r
-    // at chunk c ^ (r & 31), which spreads the 32 rows of one write over the
-    // banks) and stores whole rows: D*4 contiguous bytes per row, 1024/D rows
-    // an instruction.
-    constexpr int CHR = D / 4;  // 16-byte chunks in a row of D floats
-    if constexpr (NST * G::STAGE * 2 >= WAVES * ROWS_PER_WAVE * D * 4) {
+    // (l/32)*4 + [0,4) of row l%32 (of the wave's dims), so a direct 16-byte
+    // store touches 64 rows (cache lines) per instruction.  Where the stages
+    // have room, each wave instead writes its 32 rows x DW block into LDS
+    // (16-byte chunk c of row r at chunk c ^ (r & 31), which spreads the 32
+    // rows of one write over the banks) and stores whole row pieces: DW*4
+    // contiguous bytes per row, 1024/DW rows an instruction.
+    constexpr int CHR = DW / 4;  // 16-byte chunks in a row of DW floats
+    if constexpr (NST * G::STAGE * 2 >= NW * ROWS_PER_WAVE * DW * 4) {
         // every wave is past its last stage read (the loop ended with a barrier)
-        float *ob = reinterpret_cast<float *>(smem) + wave * (ROWS_PER_WAVE * D);
+        float *ob = reinterpret_cast<float *>(smem) + wave * (ROWS_PER_WAVE * DW);
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < DW / 32; ++dt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int c = dt * 8 + j * 2 + lhi;
                 const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
                                  acc_o[dt][j * 4 + 3] * sc};
-                *reinterpret_cast<f32x4 *>(ob + lrow * D + ((c ^ (lrow & (CHR - 1) & 31)) << 2)) = v;
+                *reinterpret_cast<f32x4 *>(ob + lrow * DW + ((c ^ (lrow & (CHR - 1) & 31)) << 2)) = v;
             }
         constexpr int RPI = 64 / CHR;  // rows per store instruction
         constexpr int NI = ROWS_PER_WAVE / RPI;
@@ -1117,14 +1145,14 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int r = i * RPI + sub;
-            rv[i] = *reinterpret_cast<const f32x4 *>(ob + r * D + ((c ^ (r & (CHR - 1) & 31)) << 2));
+            rv[i] = *reinterpret_cast<const f32x4 *>(ob + r * DW + ((c ^ (r & (CHR - 1) & 31)) << 2));
         }
         __builtin_amdgcn_sched_barrier(0);
         // lane r < 32 holds the destination (element offset) of row r of the
         // wave, -1 past the last row; a store takes its rows' offsets by lane
         // reads (scalar when one row fills the instruction)
         int64_t dst_off = -1;
-        if (row_ok) dst_off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
+        if (row_ok) dst_off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + dh * DW;
         const uint32_t off_lo = (uint32_t)dst_off, off_hi = (uint32_t)((uint64_t)dst_off >> 32);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -1147,9 +1175,9 @@ __global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_ke
         }
     } else {
         if (!row_ok) return;
-        const int64_t off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
+        const int64_t off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + dh * DW;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
+        for (int dt = 0; dt < DW / 32; ++dt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
@@ -1207,7 +1235,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(KParams p) {
                 const f32x4 ml = *reinterpret_cast<const f32x4 *>(p.ws_ml + (u + row) * 4);
                 ms[s] = ml[0];
                 ls[s] = ml[1];
-                ks[s] = (int)ml[2];
+                ks[s] = (int)ml[2 + (cg * NCH * 8 >= D / 2 ? 1 : 0)];  // the scale of this chunk's half
                 const uint16_t *src = p.ws_o + (u + blk * 32) * D + (cg * NCH * 64 + lane) * 4;
 #pragma unroll
                 for (int j = 0; j < NCH; ++j) os[s][j] = *reinterpret_cast<const u32x2 *>(src + j * 256);
@@ -1443,10 +1471,13 @@ hipError_t dispatch_pbf16(const KParams &kp, int mask, bool valid, bool qf32, hi
     }
 }
 
+// Row tiles at head_dim 256 with DMA staging run eight waves (two a SIMD, each
+// half of the output dims); the rest four.
 template <int D, int MASK, int LD, bool QF32>
 hipError_t launch_kernel(const KParams &kp, hipStream_t stream) {
     const int grid = (kp.total_wg + 7) / 8 * 8;
-    hipLaunchKernelGGL((paged_attn_kernel<D, MASK, LD, QF32>), dim3(grid), dim3(256), 0, stream, kp);
+    constexpr int NW = D == 256 && LD == LD_DMA ? 2 * WAVES : WAVES;
+    hipLaunchKernelGGL((paged_attn_kernel<D, MASK, LD, QF32, NW>), dim3(grid), dim3(64 * NW), 0, stream, kp);
     return hipGetLastError();
 }
 
