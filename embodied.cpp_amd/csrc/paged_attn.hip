@@ -952,20 +952,50 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     // straight into the MFMA operands, P in f32 split into two bf16 parts
     // (P_hi + P_lo carries 16 bits), P.V as two bf16 MFMAs.  No LDS, no
     // barrier: the other waves of the workgroup go on to the epilogue.
-    if (wave_live) {
-        float amax = 0.0f;
-        bool fin = true;
+    {
+        bool bad = false;
+        if constexpr (NW == WAVES) {
+            if (wave_live) {
+                float amax = 0.0f;
+                bool fin = true;
 #pragma unroll
-        for (int dt = 0; dt < DW / 32; ++dt)
+                for (int dt = 0; dt < DW / 32; ++dt)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                fin = fin && __builtin_isfinite(acc_o[dt][e]);
-                amax = fmaxf(amax, fabsf(acc_o[dt][e]));
+                    for (int e = 0; e < 16; ++e) {
+                        fin = fin && __builtin_isfinite(acc_o[dt][e]);
+                        amax = fmaxf(amax, fabsf(acc_o[dt][e]));
+                    }
+                float a, c;
+                half_pair(amax, a, c);
+                amax = fmaxf(a, c);
+                bad = row_ok && l_run > 0.0f && (!fin || amax < EXACT_TINY * l_run);
             }
-        float a, c;
-        half_pair(amax, a, c);
-        amax = fmaxf(a, c);
-        const bool bad = row_ok && l_run > 0.0f && (!fin || amax < EXACT_TINY * l_run);
+        } else {
+            // The row's largest |O| (+inf where a value is not finite) over
+            // both halves of its dims, so that a row is recomputed exactly
+            // when the four-wave kernel would recompute it.  (Every wave meets
+            // the barrier; the table segment's LDS is free after the loop.)
+            float amax = 0.0f;
+            bool fin = true;
+            if (wave_live) {
+#pragma unroll
+                for (int dt = 0; dt < DW / 32; ++dt)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        fin = fin && __builtin_isfinite(acc_o[dt][e]);
+                        amax = fmaxf(amax, fabsf(acc_o[dt][e]));
+                    }
+            }
+            amax = fin ? amax : INFINITY;
+            float a, c;
+            half_pair(amax, a, c);
+            amax = fmaxf(a, c);
+            float *xa = reinterpret_cast<float *>(pt);
+            if (lhi == 0) xa[wave * 32 + lrow] = amax;
+            __syncthreads();
+            amax = fmaxf(amax, xa[(wave ^ WAVES) * 32 + lrow]);
+            bad = wave_live && row_ok && l_run > 0.0f && (amax == INFINITY || amax < EXACT_TINY * l_run);
+        }
         if (__builtin_amdgcn_ballot_w64(bad) != 0) {
             // the query fragment again (reloaded rather than kept live past the
             // loop, where it would cost the loop registers)
@@ -1062,6 +1092,7 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
                     }
                 }
             }
+            float a, c;
             half_pair(l_x, a, c);
             l_run = a + c;
             m_run = m_x;
@@ -1079,41 +1110,52 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     // (Rows past the end carry values nothing reads.)
     if (ns_seq > 1) {
         const int64_t unit_row0 = ((int64_t)(b * p.hkv + kvh) * p.splits + split) * ((int64_t)p.row_tiles * ROWS_PER_WG);
-        float omax = 0.0f;  // over the wave's dims: with two halves, each has its own scale
+        // A power-of-two scale per half of the dims (dims [0, D/2) and
+        // [D/2, D)), from that half's largest |O/l|: the same partials whether
+        // one wave holds both halves or each half has its own wave.
+        constexpr int HB = D / 64;  // 32-dim blocks in a half
+        float om[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int dt = 0; dt < DW / 32; ++dt)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) omax = fmaxf(omax, fabsf(acc_o[dt][e]));
-        {
+            for (int e = 0; e < 16; ++e) {
+                const int h = dt0 + dt >= HB ? 1 : 0;
+                om[h] = fmaxf(om[h], fabsf(acc_o[dt][e]));
+            }
+        int kh[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
             float a, c;
-            half_pair(omax, a, c);
-            omax = fmaxf(a, c) * sc;
+            half_pair(om[h], a, c);
+            const float omax = fmaxf(a, c) * sc;
+            int ex = 0;
+            if (omax > 0.0f && __builtin_isfinite(omax)) frexpf(omax, &ex);
+            kh[h] = omax > 0.0f ? min(max(ex - 15, -100), 100) : 0;  // omax * 2^-k in [2^14, 2^15)
         }
-        int ex = 0;
-        if (omax > 0.0f && __builtin_isfinite(omax)) frexpf(omax, &ex);
-        const int k = omax > 0.0f ? min(max(ex - 15, -100), 100) : 0;  // omax * 2^-k in [2^14, 2^15)
         if (row_ok && lhi == 0) {
             const int64_t rowi = unit_row0 + my_row;
             const float m_out = m_run == -INFINITY ? -INFINITY : m_run * p.c_log2;
             if constexpr (NW == WAVES) {
-                *reinterpret_cast<f32x4 *>(p.ws_ml + rowi * 4) = f32x4{m_out, l_run, (float)k, (float)k};
+                *reinterpret_cast<f32x4 *>(p.ws_ml + rowi * 4) = f32x4{m_out, l_run, (float)kh[0], (float)kh[1]};
             } else {
                 // (m, l) from the first half (the halves hold the same values), each half's scale
                 if (dh == 0) *reinterpret_cast<f32x2 *>(p.ws_ml + rowi * 4) = f32x2{m_out, l_run};
-                p.ws_ml[rowi * 4 + 2 + dh] = (float)k;
+                p.ws_ml[rowi * 4 + 2 + dh] = (float)kh[dh];
             }
         }
         if (wave_live) {
-            const float scs = ldexpf(sc, -k);
+            const float scs[2] = {ldexpf(sc, -kh[0]), ldexpf(sc, -kh[1])};
             uint16_t *blk = p.ws_o + (unit_row0 + row0 + rbw * ROWS_PER_WAVE) * D + lane * 4;
 #pragma unroll
-            for (int dt = 0; dt < DW / 32; ++dt)
+            for (int dt = 0; dt < DW / 32; ++dt) {
+                const float f = scs[dt0 + dt >= HB ? 1 : 0];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const f32x4 v = {acc_o[dt][j * 4] * scs, acc_o[dt][j * 4 + 1] * scs, acc_o[dt][j * 4 + 2] * scs,
-                                     acc_o[dt][j * 4 + 3] * scs};
+                    const f32x4 v = {acc_o[dt][j * 4] * f, acc_o[dt][j * 4 + 1] * f, acc_o[dt][j * 4 + 2] * f,
+                                     acc_o[dt][j * 4 + 3] * f};
                     *reinterpret_cast<u32x2 *>(blk + ((dt0 + dt) * 4 + j) * 256) = f16x4_bits(v);
                 }
+            }
         }
         return;
     }

@@ -181,3 +181,24 @@ def test_faces_any_v_range(emb, orc, torch_dev, name, vs):
     emb.ggml_flash_attn_ext(qdd, kdd, vdd, None, odd, 0.125)
     torch.cuda.synchronize()
     assert_close(og.cpu().numpy() / vs, refg / vs, f"ggml {name}")
+
+
+def test_dim_halves_of_different_magnitude(emb, orc, torch_dev):
+    """V dims [0, 128) scaled by 1e-2 and dims [128, 256) by 1e3 (cfg1-like
+    shape, split-K 1 and 3).  The head_dim-256 row tiles give each half of the
+    output dims to its own wave, and split partials carry a power-of-two scale
+    per half (2^17 apart here): each half is held to the bar relative to its
+    own magnitude, so a half merged with the other half's scale would fail."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(0xD1A5)
+    dscale = np.concatenate([np.full(128, 1e-2), np.full(128, 1e3)])[None, None, :]
+    s = Seqs(orc, rng, [867, 300], [51, 20], 8, 1, 256, v_scale=lambda k: dscale)
+    for splits in (1, 3):
+        got = s.run(emb, torch, dev, 1 / 16, splits=splits)
+        for b in range(2):
+            ref = s.oracle(orc, b, 1 / 16)
+            for h, sl in enumerate((slice(0, 128), slice(128, 256))):
+                mag = float(np.abs(ref[..., sl]).max())
+                assert_close(got[b][..., sl] / mag, ref[..., sl] / mag, f"splits={splits} b={b} dims half {h}")
+                if s.ks_out is not None:
+                    assert_close(s.ks_out[b][..., sl] / mag, ref[..., sl] / mag, f"key-split b={b} dims half {h}")
