@@ -148,6 +148,10 @@ struct KParams {
     // [batch*hkv][splits][row_tiles*128][4]: m (log2 units), l, k0, k1 (dims
     // [0, D/2) of O/l stored as O/l * 2^-k0, dims [D/2, D) with 2^-k1)
     float *ws_ml;
+    // host choice for the head_dim-256 DMA row tiles: eight waves (two a
+    // SIMD, lower latency per tile) when the grid fits one round on the CUs,
+    // four (no repeated score MFMAs) when workgroups queue for CUs anyway
+    int32_t eight_waves;
 };
 
 // Two bf16 (packed in a dword) -> two f16 (packed in a dword), round to nearest even.
@@ -1514,12 +1518,18 @@ hipError_t dispatch_pbf16(const KParams &kp, int mask, bool valid, bool qf32, hi
 }
 
 // Row tiles at head_dim 256 with DMA staging run eight waves (two a SIMD, each
-// half of the output dims); the rest four.
+// half of the output dims) when the host asks for it; otherwise four.
 template <int D, int MASK, int LD, bool QF32>
 hipError_t launch_kernel(const KParams &kp, hipStream_t stream) {
     const int grid = (kp.total_wg + 7) / 8 * 8;
-    constexpr int NW = D == 256 && LD == LD_DMA ? 2 * WAVES : WAVES;
-    hipLaunchKernelGGL((paged_attn_kernel<D, MASK, LD, QF32, NW>), dim3(grid), dim3(64 * NW), 0, stream, kp);
+    if constexpr (D == 256 && LD == LD_DMA) {
+        if (kp.eight_waves) {
+            hipLaunchKernelGGL((paged_attn_kernel<D, MASK, LD, QF32, 2 * WAVES>), dim3(grid), dim3(128 * WAVES), 0,
+                               stream, kp);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((paged_attn_kernel<D, MASK, LD, QF32, WAVES>), dim3(grid), dim3(64 * WAVES), 0, stream, kp);
     return hipGetLastError();
 }
 
@@ -1680,13 +1690,17 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     // Automatic choice: the key-split kernel reads every K/V tile once per 32
     // rows instead of once per 128, so it pays off only while the row tiles
     // would leave most of the GPU idle (at most half the CUs busy unsplit).
-    bool ks_auto = false;
-    if (ks_ok && a->kernel == EMB_ATTN_AUTO && rows_per_unit <= 512) {
-        int dev = 0, n_cu = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
-            ks_auto = 2 * (int64_t)a->batch * a->hkv * kp.row_tiles <= n_cu;
+    int n_cu = 0;
+    {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n_cu = 0;
     }
+    bool ks_auto = false;
+    if (ks_ok && a->kernel == EMB_ATTN_AUTO && rows_per_unit <= 512 && n_cu > 0)
+        ks_auto = 2 * (int64_t)a->batch * a->hkv * kp.row_tiles <= n_cu;
+    kp.eight_waves = n_cu > 0 && kp.total_wg <= n_cu;
     if (ks_ok && (a->kernel == EMB_ATTN_KEY_SPLIT || ks_auto)) {
         KsParams ks{};
         ks.q = kp.q;
