@@ -1048,6 +1048,7 @@ def main():
         return
     if args.only == "cfg2_attn":  # prefill attention, 18 layers, split 1
         P = PagedLayers(c, 0xE3BD0001, [0] * 18, 816, 8, 1, 256, n_steps=1)
+        P.append(0, c.stream)  # the prefix K/V (a zero pool would take the exact recompute path)
         P.set_splits(1)
         for _ in range(args.warmup + args.steps):
             P.attend(0, c.stream, 1 / 16)
