@@ -234,9 +234,11 @@ struct DmaPlan {
     uint32_t koff[NB], voff[NB];
     int wave;
 
-    __device__ __forceinline__ void init() {
+    __device__ __forceinline__ void init() { init_as(threadIdx.x >> 6); }
+    // as wave w of the NW that share the copies
+    __device__ __forceinline__ void init_as(int w) {
         const int lane = threadIdx.x & 63;
-        wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        wave = __builtin_amdgcn_readfirstlane(w);
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             const int b = j * NW + wave;
@@ -503,6 +505,11 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     constexpr int NST = LD == LD_DMA && wg_per_cu<D, MASK, LD, NW>() < 3 ? 4 : 3;
     __shared__ __attribute__((aligned(16))) uint16_t smem[NST * G::STAGE];
     __shared__ __attribute__((aligned(16))) int32_t pt[VALID ? 4 : SEG_PAGES];
+    // Eight waves: the lower half's P of the current tile for the upper half
+    // (each lane's two f16x8 P.V operands), and its rescale factor per row.
+    constexpr bool SPLIT_ROLES = NW > WAVES;
+    __shared__ __attribute__((aligned(16))) f16x8 px[SPLIT_ROLES ? WAVES * 64 * 2 : 1];
+    __shared__ float pxa[SPLIT_ROLES ? WAVES * 32 : 1];
 
     // XCD-aware order: hardware ids go round-robin over the 8 XCDs, so logical
     // work ids are handed out in contiguous runs per XCD, keeping the row tiles
@@ -646,6 +653,9 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     // DMA staging: copies straight into a stage (the lane offsets are fixed).
     DmaPlan<D, NW> dma;
     if constexpr (LD == LD_DMA) dma.init();
+    // with eight waves the loop's copies are the upper half's alone
+    DmaPlan<D, WAVES> dma_up;
+    if constexpr (SPLIT_ROLES) dma_up.init_as(wave & (WAVES - 1));
     const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
     // LDS table offset of tile tt's page ids, reloading the next segment when
     // tt leaves the current one (a uniform call with a barrier; every wave is
@@ -792,9 +802,11 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     pin_q();
     __syncthreads();
     f32x16 s_cur[G::KB];
-    if (wave_live) qk(smem, s_cur);
+    // (with eight waves only the lower half computes scores)
+    const bool s_wave = wave_live && (!SPLIT_ROLES || dh == 0);
+    if (s_wave) qk(smem, s_cur);
     float mt_cur = -INFINITY;  // row max of the current tile (masked)
-    if (wave_live && t_lo < t_hi) {
+    if (s_wave && t_lo < t_hi) {
         apply_mask(s_cur, t_lo * G::KT);
         mt_cur = tile_max(s_cur);
     }
@@ -831,6 +843,138 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
         const int nx1 = cur + 1 == NST ? 0 : cur + 1;
         const int nxl = cur == 0 ? NST - 1 : cur - 1;  // receives tile t + NST - 1
         const bool more = t + NST - 1 < t_hi;
+        if constexpr (SPLIT_ROLES) {
+            // Eight waves.  Phase A: the lower half (dh 0) runs the rescale
+            // check, the S MFMAs of tile t+1 with the softmax of tile t
+            // between them, and publishes P of tile t and the rescale factors;
+            // the upper half builds the descriptors of tile t + NST - 1 and
+            // issues all its copies (into stage nxl, which no wave reads this
+            // tile).  Barrier.  Phase B: both halves run P.V of tile t on
+            // their dims (the lower half with the mask and row max of tile
+            // t+1 between the MFMAs).  The S MFMAs are done once, and the
+            // descriptor and copy work no longer sits on the S path.
+            using DPU = DmaPlan<D, WAVES>;
+            int32_t seg_pi = 0;
+            if (more) seg_pi = seg_index(t + NST - 1);  // uniform: every wave
+            const uint32_t st_l = smem_lds + nxl * (G::STAGE * 2);
+            const uint16_t *stk = smem + nx1 * G::STAGE;
+            const uint16_t *stv = smem + cur * G::STAGE;
+            auto read_k = [&](int i) {
+                return *reinterpret_cast<const u32x4 *>(&stk[k_off<D>((i / KS) * 32 + lrow, (i % KS) * 2 + lhi)]);
+            };
+            auto read_v = [&](int i) {  // i = (kb*2 + pg) * (DW/32) + dt, dims (dt0 + dt)*32 + [0, 32)
+                return *reinterpret_cast<const u32x4 *>(
+                    &stv[v_off<D>(i / (DW / 32), (dt0 + i % (DW / 32)) * 32 + lrow, lhi)]);
+            };
+            f32x16 s_nxt[G::KB];
+            f16x8 pf[G::KB][2];
+            f16x8 *pxw = px + (rbw * 64 + lane) * (2 * G::KB);
+            if (dh == 0) {
+                if (wave_live) {
+                    float alpha = 1.0f;
+                    if (__builtin_amdgcn_ballot_w64(mt_cur > m_run + p.th_raw) != 0) {
+                        const float m_new = fmaxf(m_run, mt_cur);
+                        alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
+#pragma unroll
+                        for (int i = 0; i < DW / 32; ++i) acc_o[i] *= alpha;
+                        l_run *= alpha;
+                        m_run = m_new;
+                    }
+                    if (lhi == 0) pxa[rbw * 32 + lrow] = alpha;
+                    const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * p.c_log2;
+                    u32x4 kbuf[AHEAD];
+#pragma unroll
+                    for (int i = 0; i < AHEAD; ++i) kbuf[i] = read_k(i);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < NS; ++i) {
+                        const int kb = i / KS, kk = i % KS;
+                        s_nxt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kbuf[i % AHEAD]),
+                                                                           qf[kk], kk == 0 ? f32x16{} : s_nxt[kb], 0, 0,
+                                                                           0);
+                        if (i + AHEAD < NS) kbuf[i % AHEAD] = read_k(i + AHEAD);
+#pragma unroll
+                        for (int u = 0; u < EPS; ++u) {
+                            const int el = i * EPS + u, eb = el / 16, r = el % 16;
+                            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[eb][r], p.c_log2, neg_mc));
+                            pf[eb][r >> 3][r & 7] = (_Float16)e;
+                            if (r & 1)
+                                l_run = __builtin_amdgcn_fdot2(f16x2{pf[eb][r >> 3][(r & 7) - 1], pf[eb][r >> 3][r & 7]},
+                                                               f16x2{(_Float16)1.0f, (_Float16)1.0f}, l_run, false);
+                        }
+                        asm volatile("" : "+v"(l_run));
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+#pragma unroll
+                    for (int kb = 0; kb < G::KB; ++kb) {
+                        pxw[kb * 2] = pf[kb][0];
+                        pxw[kb * 2 + 1] = pf[kb][1];
+                    }
+                }
+            } else {
+                typename DPU::Descs dsc;
+                if (more)
+                    dma_up.prepare(p, pt + seg_pi, (t + NST - 1) * G::KT, lim, kvh, dsc);
+                else
+                    dma_up.empty(dsc);
+#pragma unroll
+                for (int n = 0; n < DPU::PER_TILE; ++n) dma_up.copy(dsc, st_l, n);
+            }
+            __syncthreads();  // P of tile t and its rescale factors are published
+            if (wave_live) {
+                if (dh == 1) {
+                    const float alpha = pxa[rbw * 32 + lrow];
+                    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+                        for (int i = 0; i < DW / 32; ++i) acc_o[i] *= alpha;
+                    }
+#pragma unroll
+                    for (int kb = 0; kb < G::KB; ++kb) {
+                        pf[kb][0] = pxw[kb * 2];
+                        pf[kb][1] = pxw[kb * 2 + 1];
+                    }
+                } else if (t + 1 < t_hi) {
+                    apply_mask(s_nxt, (t + 1) * G::KT);
+                }
+                float mt_nxt = -INFINITY;
+                u32x4 vbuf[AHEAD];
+#pragma unroll
+                for (int i = 0; i < AHEAD; ++i) vbuf[i] = read_v(i);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < NPV; ++i) {
+                    const int kp = i / (DW / 32), dt = i % (DW / 32);
+                    acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vbuf[i % AHEAD]),
+                                                                      pf[kp >> 1][kp & 1], acc_o[dt], 0, 0, 0);
+                    if (i + AHEAD < NPV) vbuf[i % AHEAD] = read_v(i + AHEAD);
+                    if (dh == 0) {
+#pragma unroll
+                        for (int u = 0; u < EPV; ++u) {
+                            const int el = i * EPV + u;
+                            mt_nxt = fmaxf(mt_nxt, s_nxt[el / 16][el % 16]);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (dh == 0) {
+                    float a, c;
+                    half_pair(mt_nxt, a, c);
+                    mt_cur = fmaxf(a, c);
+#pragma unroll
+                    for (int kb = 0; kb < G::KB; ++kb) s_cur[kb] = s_nxt[kb];
+                }
+            }
+            // (upper half) tile t+2 has landed; with four stages tile t+3,
+            // issued this tile, may still fly; after the last tile nothing may
+            if (dh == 1) {
+                if (t + 1 < t_hi)
+                    wait_vmcnt<(NST - 3) * DPU::PER_TILE>();
+                else
+                    wait_vmcnt<0>();
+            }
+            __syncthreads();
+            continue;
+        }
         typename DP::Descs dsc;
         const uint32_t st_l = smem_lds + nxl * (G::STAGE * 2);
         if constexpr (LD == LD_DMA) {
@@ -996,8 +1140,20 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
             amax = fmaxf(a, c);
             float *xa = reinterpret_cast<float *>(pt);
             if (lhi == 0) xa[wave * 32 + lrow] = amax;
+            // the running max and sum live in the lower half (the upper half
+            // computed no scores): published with the maxima (the P handoff
+            // buffer is free after the loop)
+            float *xm = reinterpret_cast<float *>(px);
+            if (dh == 0 && lhi == 0) {
+                xm[rbw * 32 + lrow] = l_run;
+                xm[WAVES * 32 + rbw * 32 + lrow] = m_run;
+            }
             __syncthreads();
             amax = fmaxf(amax, xa[(wave ^ WAVES) * 32 + lrow]);
+            if (dh == 1) {
+                l_run = xm[rbw * 32 + lrow];
+                m_run = xm[WAVES * 32 + rbw * 32 + lrow];
+            }
             bad = wave_live && row_ok && l_run > 0.0f && (amax == INFINITY || amax < EXACT_TINY * l_run);
         }
         if (__builtin_amdgcn_ballot_w64(bad) != 0) {
