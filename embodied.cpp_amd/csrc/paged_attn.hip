@@ -76,7 +76,7 @@ namespace {
 using namespace emb_attn;
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int WAVES = 4;  // row blocks of a workgroup
+constexpr int WAVES = 4;
 constexpr int ROWS_PER_WAVE = 32;
 constexpr int ROWS_PER_WG = WAVES * ROWS_PER_WAVE;
 constexpr int SEG_PAGES = 1024;  // block-table entries held in LDS at a time (16384 keys)
@@ -148,10 +148,6 @@ struct KParams {
     // [batch*hkv][splits][row_tiles*128][4]: m (log2 units), l, k0, k1 (dims
     // [0, D/2) of O/l stored as O/l * 2^-k0, dims [D/2, D) with 2^-k1)
     float *ws_ml;
-    // host choice for the head_dim-256 DMA row tiles: eight waves (two a
-    // SIMD, lower latency per tile) when the grid fits one round on the CUs,
-    // four (no repeated score MFMAs) when workgroups queue for CUs anyway
-    int32_t eight_waves;
 };
 
 // Two bf16 (packed in a dword) -> two f16 (packed in a dword), round to nearest even.
@@ -219,35 +215,32 @@ __device__ __forceinline__ void page_rsrc(const KParams &p, const uint16_t *vbas
 
 
 // DMA path: the tile's K rows and f16 V-shadow pages go straight into the
-// stage.  Wave w of NW copies 1 KB blocks b = NW*j + w of each image; block b of the
+// stage.  Wave w copies 1 KB blocks b = 4j + w of each image; block b of the
 // K image holds key rows [b*64/CH, (b+1)*64/CH), so lane i loads the global
 // chunk that the XOR swizzle puts at slot (b*64 + i) % CH of its row.  A block
 // never crosses a page, so one descriptor serves all 64 lanes.  The per-lane
 // byte offsets do not depend on the tile and are computed once.
-template <int D, int NW = WAVES>
+template <int D>
 struct DmaPlan {
     using G = Geo<D>;
-    static_assert(G::BLOCKS % NW == 0, "copies must split evenly over the waves");
-    static constexpr int NB = G::BLOCKS / NW;  // blocks per wave and image
+    static constexpr int NB = G::BLOCKS / 4;  // blocks per wave and image
     static constexpr int PER_TILE = 2 * NB;   // copies per wave and tile
     static constexpr int RB = 64 / G::CH;     // key rows per K block
     uint32_t koff[NB], voff[NB];
     int wave;
 
-    __device__ __forceinline__ void init() { init_as(threadIdx.x >> 6); }
-    // as wave w of the NW that share the copies
-    __device__ __forceinline__ void init_as(int w) {
+    __device__ __forceinline__ void init() {
         const int lane = threadIdx.x & 63;
-        wave = __builtin_amdgcn_readfirstlane(w);
+        wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const int b = j * NW + wave;
+            const int b = j * 4 + wave;
             const int q = b * 64 + lane;
             const int r = q / G::CH, sl = q % G::CH;
             const int c = sl ^ (r & G::SWZ);
             koff[j] = ((r & 15) * D + c * 8) * 2;
             // V image: page pp covers blocks [pp*D/32, (pp+1)*D/32)
-            const int pp = D >= 128 ? (j * NW * 32) / D : 2 * j + (wave >> 1);
+            const int pp = D >= 128 ? (j * 4 * 32) / D : 2 * j + (wave >> 1);
             voff[j] = b * 1024 - pp * D * 32 + lane * 16;
         }
     }
@@ -287,24 +280,23 @@ struct DmaPlan {
     }
 
     // Copy n of this wave's PER_TILE copies of a tile into the stage at LDS
-    // byte address st: n < NB is K block NW*n + w, the rest V blocks.
+    // byte address st: n < NB is K block 4n + w, the rest V blocks.
     __device__ __forceinline__ void copy(const Descs &ds, uint32_t st, int n) const {
         if (n < NB) {
-            const int j = n, b = j * NW + wave;
+            const int j = n, b = j * 4 + wave;
             u32x4 dk;
-            // page of K block b = (NW*j + w) * RB / 16: j*NW*RB/16 while
-            // NW*RB <= 16 (w < NW), 2j + w/2 for RB = 8 (D = 64, NW = 4)
-            static_assert(NW * RB <= 16 || (RB == 8 && NW == 4), "K block page");
-            if constexpr (NW * RB <= 16)
-                dk = ds.kd[(j * NW * RB) / 16];
+            // page of K block b = (4j + w) * RB / 16: j*RB/4 for RB <= 4 (w < 4),
+            // 2j + w/2 for RB = 8 (D = 64)
+            if constexpr (RB <= 4)
+                dk = ds.kd[(j * RB) / 4];
             else
                 dk = (wave >> 1) ? ds.kd[2 * j + 1] : ds.kd[2 * j];
             lds_copy16(dk, __builtin_amdgcn_readfirstlane(st + b * 1024), koff[j]);
         } else {
-            const int j = n - NB, b = j * NW + wave;
+            const int j = n - NB, b = j * 4 + wave;
             u32x4 dv;
             if constexpr (D >= 128)
-                dv = ds.vd[(j * NW * 32) / D];
+                dv = ds.vd[(j * 4 * 32) / D];
             else
                 dv = (wave >> 1) ? ds.vd[2 * j + 1] : ds.vd[2 * j];
             lds_copy16(dv, __builtin_amdgcn_readfirstlane(st + G::K_ELEMS * 2 + b * 1024), voff[j]);
@@ -461,12 +453,10 @@ struct RegLoader {
     }
 };
 
-// pt[i] = page id of page index seg_p0 + i, or -1 at and past p_end, written
-// by the first 256 threads.  (All loads first, then all LDS writes: one
-// memory round trip, not four.)
+// pt[i] = page id of page index seg_p0 + i, or -1 at and past p_end.
+// (All loads first, then all LDS writes: one memory round trip, not four.)
 __device__ __forceinline__ void load_segment(const int32_t *bt_b, int32_t seg_p0, int32_t p_end, int32_t *pt) {
-    static_assert(SEG_PAGES % 256 == 0, "segment must split evenly over 256 threads");
-    if (threadIdx.x >= 256) return;
+    static_assert(SEG_PAGES % 256 == 0, "segment must split evenly over the workgroup");
     int32_t v[SEG_PAGES / 256];
 #pragma unroll
     for (int k = 0; k < SEG_PAGES / 256; ++k) {
@@ -482,34 +472,20 @@ __device__ __forceinline__ void load_segment(const int32_t *bt_b, int32_t seg_p0
 // values that do not fit live outside the key loop): a third wave per SIMD
 // hides more of each tile's latency.  The masked and register-staged
 // variants would spill inside the loop there, so they keep two.
-template <int D, int MASK, int LD, int NW = WAVES>
+template <int D, int MASK, int LD>
 constexpr int wg_per_cu() {
-    if constexpr (NW > WAVES) return 1;
     return D == 128 && LD == LD_DMA && MASK == EMB_MASK_FULL ? 3 : Geo<D>::MIN_WG;
 }
 
-// NW = 4: wave w owns row block w and all D output dims.  NW = 8 (head_dim
-// 256, DMA staging): wave w owns row block w % 4 and half w / 4 of the output
-// dims; both halves of a row block compute the same scores and softmax (so
-// they agree bit for bit on the running max and sum), each its own half of
-// P.V.  Half the accumulators and the query in AGPRs fit a wave into 256
-// registers: two waves per SIMD instead of one, each with half the P.V work.
-template <int D, int MASK, int LD, bool QF32, int NW>
-__global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged_attn_kernel(KParams p) {
+template <int D, int MASK, int LD, bool QF32>
+__global__ __launch_bounds__(256, (wg_per_cu<D, MASK, LD>())) void paged_attn_kernel(KParams p) {
     using G = Geo<D>;
     constexpr bool VALID = LD == LD_VALID;
-    static_assert(NW == WAVES || (NW == 2 * WAVES && LD == LD_DMA && D == 256), "eight waves: D 256, DMA staging");
-    constexpr int DW = NW == WAVES ? D : D / 2;  // output dims of a wave
     // four stages when the copies bypass registers (a tile's loads get two
     // iterations to land), three otherwise and where three workgroups share a CU
-    constexpr int NST = LD == LD_DMA && wg_per_cu<D, MASK, LD, NW>() < 3 ? 4 : 3;
+    constexpr int NST = LD == LD_DMA && wg_per_cu<D, MASK, LD>() < 3 ? 4 : 3;
     __shared__ __attribute__((aligned(16))) uint16_t smem[NST * G::STAGE];
     __shared__ __attribute__((aligned(16))) int32_t pt[VALID ? 4 : SEG_PAGES];
-    // Eight waves: the lower half's P of the current tile for the upper half
-    // (each lane's two f16x8 P.V operands), and its rescale factor per row.
-    constexpr bool SPLIT_ROLES = NW > WAVES;
-    __shared__ __attribute__((aligned(16))) f16x8 px[SPLIT_ROLES ? WAVES * 64 * 2 : 1];
-    __shared__ float pxa[SPLIT_ROLES ? WAVES * 32 : 1];
 
     // XCD-aware order: hardware ids go round-robin over the 8 XCDs, so logical
     // work ids are handed out in contiguous runs per XCD, keeping the row tiles
@@ -538,13 +514,10 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     const int lane = threadIdx.x & 63;
     const int lrow = lane & 31;
     const int lhi = lane >> 5;
-    const int rbw = __builtin_amdgcn_readfirstlane(wave & (WAVES - 1));  // row block of the wave
-    const int dh = NW == WAVES ? 0 : __builtin_amdgcn_readfirstlane(wave / WAVES);  // its half of the dims
-    const int dt0 = dh * (DW / 32);  // first 32-dim block of O the wave owns
-    const int32_t my_row = row0 + rbw * ROWS_PER_WAVE + lrow;
+    const int32_t my_row = row0 + wave * ROWS_PER_WAVE + lrow;
     const bool row_ok = my_row < rows;
     // a wave past the last row only helps stage tiles (and meets the barriers)
-    const bool wave_live = __builtin_amdgcn_readfirstlane(row0 + rbw * ROWS_PER_WAVE) < rows;
+    const bool wave_live = __builtin_amdgcn_readfirstlane(row0 + wave * ROWS_PER_WAVE) < rows;
     const int32_t tok = row_ok ? my_row / p.G : 0;
     const int32_t head = kvh * p.G + (row_ok ? my_row % p.G : 0);
     const int32_t qpos = qpos0 + tok;
@@ -595,9 +568,7 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     // arch VGPRs; the read-only query fragment moves to AGPRs, which MFMA reads
     // directly.  (Done once the loads have landed, so the move does not wait.)
     auto pin_q = [&]() {
-        // (not with eight waves: there every register, accumulators included,
-        // is an arch VGPR -- 256 a wave -- and the query stays among them)
-        if constexpr (D >= 256 && NW == WAVES) {
+        if constexpr (D >= 256) {
 #pragma unroll
             for (int kk = 0; kk < D / 16; ++kk) {
                 u32x4 w = __builtin_bit_cast(u32x4, qf[kk]);
@@ -636,9 +607,9 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
         full_lo = p.window >= 0 ? max(0, (qp_max / p.chunk - p.window) * p.chunk) : 0;
     }
 
-    f32x16 acc_o[DW / 32];
+    f32x16 acc_o[D / 32];
 #pragma unroll
-    for (int i = 0; i < DW / 32; ++i) acc_o[i] = f32x16{};
+    for (int i = 0; i < D / 32; ++i) acc_o[i] = f32x16{};
     float m_run = -INFINITY, l_run = 0.0f;
 
     const int32_t lim = min(nk, p.capacity);  // slots at or past the capacity are zero rows
@@ -651,11 +622,8 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     int32_t seg_len = windowed ? WIN_PAGES : SEG_PAGES;
 
     // DMA staging: copies straight into a stage (the lane offsets are fixed).
-    DmaPlan<D, NW> dma;
+    DmaPlan<D> dma;
     if constexpr (LD == LD_DMA) dma.init();
-    // with eight waves the loop's copies are the upper half's alone
-    DmaPlan<D, WAVES> dma_up;
-    if constexpr (SPLIT_ROLES) dma_up.init_as(wave & (WAVES - 1));
     const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)smem;
     // LDS table offset of tile tt's page ids, reloading the next segment when
     // tt leaves the current one (a uniform call with a barrier; every wave is
@@ -802,11 +770,9 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     pin_q();
     __syncthreads();
     f32x16 s_cur[G::KB];
-    // (with eight waves only the lower half computes scores)
-    const bool s_wave = wave_live && (!SPLIT_ROLES || dh == 0);
-    if (s_wave) qk(smem, s_cur);
+    if (wave_live) qk(smem, s_cur);
     float mt_cur = -INFINITY;  // row max of the current tile (masked)
-    if (s_wave && t_lo < t_hi) {
+    if (wave_live && t_lo < t_hi) {
         apply_mask(s_cur, t_lo * G::KT);
         mt_cur = tile_max(s_cur);
     }
@@ -823,13 +789,11 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     // AHEAD steps later, so the MFMAs never wait out the LDS latency, and the
     // copies trickle into the address unit instead of stalling all waves at
     // once at the top of the tile.
-    using DP = DmaPlan<D, NW>;
-    constexpr int KS = D / 16;                  // k-steps of one 32-key S block
-    constexpr int NS = G::KB * KS;              // S MFMAs a tile
-    constexpr int NPV = G::KB * 2 * (DW / 32);  // P.V MFMAs a tile (the wave's dims)
-    constexpr int EPS = G::KB * 16 / NS;        // score elements per S step
-    constexpr int EPV = G::KB * 16 / NPV;       // and per P.V step
-    static_assert(NS * EPS == G::KB * 16 && NPV * EPV == G::KB * 16 && 2 * DP::PER_TILE <= NPV, "tile schedule");
+    constexpr int KS = D / 16;                 // k-steps of one 32-key S block
+    constexpr int NS = G::KB * KS;             // S MFMAs a tile
+    constexpr int NPV = G::KB * 2 * (D / 32);  // P.V MFMAs a tile
+    constexpr int EPM = G::KB * 16 / NS;       // score elements per step (both phases)
+    static_assert(NPV * EPM == G::KB * 16 && 2 * DmaPlan<D>::PER_TILE <= NPV, "tile schedule");
     //
     // The loop runs NST tiles an iteration (tile t_lo + i sits in stage i %
     // NST), so every stage index is a compile-time constant: LDS addresses
@@ -843,139 +807,7 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
         const int nx1 = cur + 1 == NST ? 0 : cur + 1;
         const int nxl = cur == 0 ? NST - 1 : cur - 1;  // receives tile t + NST - 1
         const bool more = t + NST - 1 < t_hi;
-        if constexpr (SPLIT_ROLES) {
-            // Eight waves.  Phase A: the lower half (dh 0) runs the rescale
-            // check, the S MFMAs of tile t+1 with the softmax of tile t
-            // between them, and publishes P of tile t and the rescale factors;
-            // the upper half builds the descriptors of tile t + NST - 1 and
-            // issues all its copies (into stage nxl, which no wave reads this
-            // tile).  Barrier.  Phase B: both halves run P.V of tile t on
-            // their dims (the lower half with the mask and row max of tile
-            // t+1 between the MFMAs).  The S MFMAs are done once, and the
-            // descriptor and copy work no longer sits on the S path.
-            using DPU = DmaPlan<D, WAVES>;
-            int32_t seg_pi = 0;
-            if (more) seg_pi = seg_index(t + NST - 1);  // uniform: every wave
-            const uint32_t st_l = smem_lds + nxl * (G::STAGE * 2);
-            const uint16_t *stk = smem + nx1 * G::STAGE;
-            const uint16_t *stv = smem + cur * G::STAGE;
-            auto read_k = [&](int i) {
-                return *reinterpret_cast<const u32x4 *>(&stk[k_off<D>((i / KS) * 32 + lrow, (i % KS) * 2 + lhi)]);
-            };
-            auto read_v = [&](int i) {  // i = (kb*2 + pg) * (DW/32) + dt, dims (dt0 + dt)*32 + [0, 32)
-                return *reinterpret_cast<const u32x4 *>(
-                    &stv[v_off<D>(i / (DW / 32), (dt0 + i % (DW / 32)) * 32 + lrow, lhi)]);
-            };
-            f32x16 s_nxt[G::KB];
-            f16x8 pf[G::KB][2];
-            f16x8 *pxw = px + (rbw * 64 + lane) * (2 * G::KB);
-            if (dh == 0) {
-                if (wave_live) {
-                    float alpha = 1.0f;
-                    if (__builtin_amdgcn_ballot_w64(mt_cur > m_run + p.th_raw) != 0) {
-                        const float m_new = fmaxf(m_run, mt_cur);
-                        alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
-#pragma unroll
-                        for (int i = 0; i < DW / 32; ++i) acc_o[i] *= alpha;
-                        l_run *= alpha;
-                        m_run = m_new;
-                    }
-                    if (lhi == 0) pxa[rbw * 32 + lrow] = alpha;
-                    const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * p.c_log2;
-                    u32x4 kbuf[AHEAD];
-#pragma unroll
-                    for (int i = 0; i < AHEAD; ++i) kbuf[i] = read_k(i);
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int i = 0; i < NS; ++i) {
-                        const int kb = i / KS, kk = i % KS;
-                        s_nxt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kbuf[i % AHEAD]),
-                                                                           qf[kk], kk == 0 ? f32x16{} : s_nxt[kb], 0, 0,
-                                                                           0);
-                        if (i + AHEAD < NS) kbuf[i % AHEAD] = read_k(i + AHEAD);
-#pragma unroll
-                        for (int u = 0; u < EPS; ++u) {
-                            const int el = i * EPS + u, eb = el / 16, r = el % 16;
-                            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[eb][r], p.c_log2, neg_mc));
-                            pf[eb][r >> 3][r & 7] = (_Float16)e;
-                            if (r & 1)
-                                l_run = __builtin_amdgcn_fdot2(f16x2{pf[eb][r >> 3][(r & 7) - 1], pf[eb][r >> 3][r & 7]},
-                                                               f16x2{(_Float16)1.0f, (_Float16)1.0f}, l_run, false);
-                        }
-                        asm volatile("" : "+v"(l_run));
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-#pragma unroll
-                    for (int kb = 0; kb < G::KB; ++kb) {
-                        pxw[kb * 2] = pf[kb][0];
-                        pxw[kb * 2 + 1] = pf[kb][1];
-                    }
-                }
-            } else {
-                typename DPU::Descs dsc;
-                if (more)
-                    dma_up.prepare(p, pt + seg_pi, (t + NST - 1) * G::KT, lim, kvh, dsc);
-                else
-                    dma_up.empty(dsc);
-#pragma unroll
-                for (int n = 0; n < DPU::PER_TILE; ++n) dma_up.copy(dsc, st_l, n);
-            }
-            __syncthreads();  // P of tile t and its rescale factors are published
-            if (wave_live) {
-                if (dh == 1) {
-                    const float alpha = pxa[rbw * 32 + lrow];
-                    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
-#pragma unroll
-                        for (int i = 0; i < DW / 32; ++i) acc_o[i] *= alpha;
-                    }
-#pragma unroll
-                    for (int kb = 0; kb < G::KB; ++kb) {
-                        pf[kb][0] = pxw[kb * 2];
-                        pf[kb][1] = pxw[kb * 2 + 1];
-                    }
-                } else if (t + 1 < t_hi) {
-                    apply_mask(s_nxt, (t + 1) * G::KT);
-                }
-                float mt_nxt = -INFINITY;
-                u32x4 vbuf[AHEAD];
-#pragma unroll
-                for (int i = 0; i < AHEAD; ++i) vbuf[i] = read_v(i);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int i = 0; i < NPV; ++i) {
-                    const int kp = i / (DW / 32), dt = i % (DW / 32);
-                    acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vbuf[i % AHEAD]),
-                                                                      pf[kp >> 1][kp & 1], acc_o[dt], 0, 0, 0);
-                    if (i + AHEAD < NPV) vbuf[i % AHEAD] = read_v(i + AHEAD);
-                    if (dh == 0) {
-#pragma unroll
-                        for (int u = 0; u < EPV; ++u) {
-                            const int el = i * EPV + u;
-                            mt_nxt = fmaxf(mt_nxt, s_nxt[el / 16][el % 16]);
-                        }
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-                if (dh == 0) {
-                    float a, c;
-                    half_pair(mt_nxt, a, c);
-                    mt_cur = fmaxf(a, c);
-#pragma unroll
-                    for (int kb = 0; kb < G::KB; ++kb) s_cur[kb] = s_nxt[kb];
-                }
-            }
-            // (upper half) tile t+2 has landed; with four stages tile t+3,
-            // issued this tile, may still fly; after the last tile nothing may
-            if (dh == 1) {
-                if (t + 1 < t_hi)
-                    wait_vmcnt<(NST - 3) * DPU::PER_TILE>();
-                else
-                    wait_vmcnt<0>();
-            }
-            __syncthreads();
-            continue;
-        }
-        typename DP::Descs dsc;
+        typename DmaPlan<D>::Descs dsc;
         const uint32_t st_l = smem_lds + nxl * (G::STAGE * 2);
         if constexpr (LD == LD_DMA) {
             // Past the last tile the copies still run, through empty
@@ -995,7 +827,7 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
                 const float m_new = fmaxf(m_run, mt_cur);
                 const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * p.c_log2);
 #pragma unroll
-                for (int i = 0; i < DW / 32; ++i) acc_o[i] *= alpha;
+                for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
                 l_run *= alpha;
                 m_run = m_new;
             }
@@ -1005,9 +837,9 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
             auto read_k = [&](int i) {
                 return *reinterpret_cast<const u32x4 *>(&stk[k_off<D>((i / KS) * 32 + lrow, (i % KS) * 2 + lhi)]);
             };
-            auto read_v = [&](int i) {  // i = (kb*2 + pg) * (DW/32) + dt, dims (dt0 + dt)*32 + [0, 32)
+            auto read_v = [&](int i) {  // i = (kb*2 + pg) * (D/32) + dt
                 return *reinterpret_cast<const u32x4 *>(
-                    &stv[v_off<D>(i / (DW / 32), (dt0 + i % (DW / 32)) * 32 + lrow, lhi)]);
+                    &stv[v_off<D>(i / (D / 32), (i % (D / 32)) * 32 + lrow, lhi)]);
             };
             f32x16 s_nxt[G::KB];
             const float neg_mc = m_run == -INFINITY ? 0.0f : -m_run * p.c_log2;
@@ -1023,8 +855,8 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
                                                                    kk == 0 ? f32x16{} : s_nxt[kb], 0, 0, 0);
                 if (i + AHEAD < NS) kbuf[i % AHEAD] = read_k(i + AHEAD);
 #pragma unroll
-                for (int u = 0; u < EPS; ++u) {
-                    const int el = i * EPS + u, eb = el / 16, r = el % 16;
+                for (int u = 0; u < EPM; ++u) {
+                    const int el = i * EPM + u, eb = el / 16, r = el % 16;
                     const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[eb][r], p.c_log2, neg_mc));
                     pf[eb][r >> 3][r & 7] = (_Float16)e;
                     // row sum of exactly the f16 weights the P.V product uses
@@ -1046,15 +878,15 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < NPV; ++i) {
-                const int kp = i / (DW / 32), dt = i % (DW / 32);
+                const int kp = i / (D / 32), dt = i % (D / 32);
                 acc_o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vbuf[i % AHEAD]),
                                                                   pf[kp >> 1][kp & 1], acc_o[dt], 0, 0, 0);
                 if (i + AHEAD < NPV) vbuf[i % AHEAD] = read_v(i + AHEAD);
                 if constexpr (LD == LD_DMA)
-                    if ((i & 1) && (i >> 1) < DP::PER_TILE) dma.copy(dsc, st_l, i >> 1);
+                    if ((i & 1) && (i >> 1) < DmaPlan<D>::PER_TILE) dma.copy(dsc, st_l, i >> 1);
 #pragma unroll
-                for (int u = 0; u < EPV; ++u) {
-                    const int el = i * EPV + u;
+                for (int u = 0; u < EPM; ++u) {
+                    const int el = i * EPM + u;
                     mt_nxt = fmaxf(mt_nxt, s_nxt[el / 16][el % 16]);
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -1068,14 +900,14 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
             for (int kb = 0; kb < G::KB; ++kb) s_cur[kb] = s_nxt[kb];
         } else if constexpr (LD == LD_DMA) {
 #pragma unroll
-            for (int n = 0; n < DP::PER_TILE; ++n) dma.copy(dsc, st_l, n);
+            for (int n = 0; n < DmaPlan<D>::PER_TILE; ++n) dma.copy(dsc, st_l, n);
         }
         if constexpr (LD == LD_DMA) {
             // tile t+2 (needed by the next S) has landed; with four stages
             // tile t+3, issued this tile, may still fly; after the last tile
             // nothing may (the epilogue reuses the stages)
             if (t + 1 < t_hi)
-                wait_vmcnt<(NST - 3) * DP::PER_TILE>();
+                wait_vmcnt<(NST - 3) * DmaPlan<D>::PER_TILE>();
             else
                 wait_vmcnt<0>();
         } else if (more) {
@@ -1100,69 +932,27 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     // straight into the MFMA operands, P in f32 split into two bf16 parts
     // (P_hi + P_lo carries 16 bits), P.V as two bf16 MFMAs.  No LDS, no
     // barrier: the other waves of the workgroup go on to the epilogue.
-    {
-        bool bad = false;
-        if constexpr (NW == WAVES) {
-            if (wave_live) {
-                float amax = 0.0f;
-                bool fin = true;
+    if (wave_live) {
+        float amax = 0.0f;
+        bool fin = true;
 #pragma unroll
-                for (int dt = 0; dt < DW / 32; ++dt)
+        for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        fin = fin && __builtin_isfinite(acc_o[dt][e]);
-                        amax = fmaxf(amax, fabsf(acc_o[dt][e]));
-                    }
-                float a, c;
-                half_pair(amax, a, c);
-                amax = fmaxf(a, c);
-                bad = row_ok && l_run > 0.0f && (!fin || amax < EXACT_TINY * l_run);
+            for (int e = 0; e < 16; ++e) {
+                fin = fin && __builtin_isfinite(acc_o[dt][e]);
+                amax = fmaxf(amax, fabsf(acc_o[dt][e]));
             }
-        } else {
-            // The row's largest |O| (+inf where a value is not finite) over
-            // both halves of its dims, so that a row is recomputed exactly
-            // when the four-wave kernel would recompute it.  (Every wave meets
-            // the barrier; the table segment's LDS is free after the loop.)
-            float amax = 0.0f;
-            bool fin = true;
-            if (wave_live) {
-#pragma unroll
-                for (int dt = 0; dt < DW / 32; ++dt)
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        fin = fin && __builtin_isfinite(acc_o[dt][e]);
-                        amax = fmaxf(amax, fabsf(acc_o[dt][e]));
-                    }
-            }
-            amax = fin ? amax : INFINITY;
-            float a, c;
-            half_pair(amax, a, c);
-            amax = fmaxf(a, c);
-            float *xa = reinterpret_cast<float *>(pt);
-            if (lhi == 0) xa[wave * 32 + lrow] = amax;
-            // the running max and sum live in the lower half (the upper half
-            // computed no scores): published with the maxima (the P handoff
-            // buffer is free after the loop)
-            float *xm = reinterpret_cast<float *>(px);
-            if (dh == 0 && lhi == 0) {
-                xm[rbw * 32 + lrow] = l_run;
-                xm[WAVES * 32 + rbw * 32 + lrow] = m_run;
-            }
-            __syncthreads();
-            amax = fmaxf(amax, xa[(wave ^ WAVES) * 32 + lrow]);
-            if (dh == 1) {
-                l_run = xm[rbw * 32 + lrow];
-                m_run = xm[WAVES * 32 + rbw * 32 + lrow];
-            }
-            bad = wave_live && row_ok && l_run > 0.0f && (amax == INFINITY || amax < EXACT_TINY * l_run);
-        }
+        float a, c;
+        half_pair(amax, a, c);
+        amax = fmaxf(a, c);
+        const bool bad = row_ok && l_run > 0.0f && (!fin || amax < EXACT_TINY * l_run);
         if (__builtin_amdgcn_ballot_w64(bad) != 0) {
             // the query fragment again (reloaded rather than kept live past the
             // loop, where it would cost the loop registers)
             load_q();
             pin_q();
 #pragma unroll
-            for (int i = 0; i < DW / 32; ++i) acc_o[i] = f32x16{};
+            for (int i = 0; i < D / 32; ++i) acc_o[i] = f32x16{};
             float m_x = -INFINITY, l_x = 0.0f;
             // logical slot of key j (-1: a zero row), and its page
             auto slot_of = [&](int32_t j) {
@@ -1202,7 +992,7 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
                 const float m_new = fmaxf(m_x, tile_max(sx));
                 const float alpha = m_x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_x - m_new) * p.c_log2);
 #pragma unroll
-                for (int i = 0; i < DW / 32; ++i) acc_o[i] *= alpha;
+                for (int i = 0; i < D / 32; ++i) acc_o[i] *= alpha;
                 l_x *= alpha;
                 m_x = m_new;
                 const float neg = m_new == -INFINITY ? 0.0f : -m_new * p.c_log2;
@@ -1234,8 +1024,8 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
                             vr[m] = page_row(vs[m]);
                         }
 #pragma unroll
-                        for (int dt = 0; dt < DW / 32; ++dt) {
-                            const int d = (dt0 + dt) * 32 + lrow;
+                        for (int dt = 0; dt < D / 32; ++dt) {
+                            const int d = dt * 32 + lrow;
                             u32x4 vw;
 #pragma unroll
                             for (int m = 0; m < 8; m += 2) {
@@ -1252,7 +1042,6 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
                     }
                 }
             }
-            float a, c;
             half_pair(l_x, a, c);
             l_run = a + c;
             m_run = m_x;
@@ -1271,17 +1060,14 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
     if (ns_seq > 1) {
         const int64_t unit_row0 = ((int64_t)(b * p.hkv + kvh) * p.splits + split) * ((int64_t)p.row_tiles * ROWS_PER_WG);
         // A power-of-two scale per half of the dims (dims [0, D/2) and
-        // [D/2, D)), from that half's largest |O/l|: the same partials whether
-        // one wave holds both halves or each half has its own wave.
+        // [D/2, D)), from that half's largest |O/l|: a half whose values are
+        // far below the other's keeps its own 11 bits.
         constexpr int HB = D / 64;  // 32-dim blocks in a half
         float om[2] = {0.0f, 0.0f};
 #pragma unroll
-        for (int dt = 0; dt < DW / 32; ++dt)
+        for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int h = dt0 + dt >= HB ? 1 : 0;
-                om[h] = fmaxf(om[h], fabsf(acc_o[dt][e]));
-            }
+            for (int e = 0; e < 16; ++e) om[dt >= HB ? 1 : 0] = fmaxf(om[dt >= HB ? 1 : 0], fabsf(acc_o[dt][e]));
         int kh[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -1294,50 +1080,44 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
         }
         if (row_ok && lhi == 0) {
             const int64_t rowi = unit_row0 + my_row;
-            const float m_out = m_run == -INFINITY ? -INFINITY : m_run * p.c_log2;
-            if constexpr (NW == WAVES) {
-                *reinterpret_cast<f32x4 *>(p.ws_ml + rowi * 4) = f32x4{m_out, l_run, (float)kh[0], (float)kh[1]};
-            } else {
-                // (m, l) from the first half (the halves hold the same values), each half's scale
-                if (dh == 0) *reinterpret_cast<f32x2 *>(p.ws_ml + rowi * 4) = f32x2{m_out, l_run};
-                p.ws_ml[rowi * 4 + 2 + dh] = (float)kh[dh];
-            }
+            *reinterpret_cast<f32x4 *>(p.ws_ml + rowi * 4) =
+                f32x4{m_run == -INFINITY ? -INFINITY : m_run * p.c_log2, l_run, (float)kh[0], (float)kh[1]};
         }
         if (wave_live) {
             const float scs[2] = {ldexpf(sc, -kh[0]), ldexpf(sc, -kh[1])};
-            uint16_t *blk = p.ws_o + (unit_row0 + row0 + rbw * ROWS_PER_WAVE) * D + lane * 4;
+            uint16_t *blk = p.ws_o + (unit_row0 + row0 + wave * ROWS_PER_WAVE) * D + lane * 4;
 #pragma unroll
-            for (int dt = 0; dt < DW / 32; ++dt) {
-                const float f = scs[dt0 + dt >= HB ? 1 : 0];
+            for (int dt = 0; dt < D / 32; ++dt) {
+                const float f = scs[dt >= HB ? 1 : 0];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const f32x4 v = {acc_o[dt][j * 4] * f, acc_o[dt][j * 4 + 1] * f, acc_o[dt][j * 4 + 2] * f,
                                      acc_o[dt][j * 4 + 3] * f};
-                    *reinterpret_cast<u32x2 *>(blk + ((dt0 + dt) * 4 + j) * 256) = f16x4_bits(v);
+                    *reinterpret_cast<u32x2 *>(blk + (dt * 4 + j) * 256) = f16x4_bits(v);
                 }
             }
         }
         return;
     }
     // Output rows, the normalised O (f32).  Lane l holds dims dt*32 + j*8 +
-    // (l/32)*4 + [0,4) of row l%32 (of the wave's dims), so a direct 16-byte
-    // store touches 64 rows (cache lines) per instruction.  Where the stages
-    // have room, each wave instead writes its 32 rows x DW block into LDS
-    // (16-byte chunk c of row r at chunk c ^ (r & 31), which spreads the 32
-    // rows of one write over the banks) and stores whole row pieces: DW*4
-    // contiguous bytes per row, 1024/DW rows an instruction.
-    constexpr int CHR = DW / 4;  // 16-byte chunks in a row of DW floats
-    if constexpr (NST * G::STAGE * 2 >= NW * ROWS_PER_WAVE * DW * 4) {
+    // (l/32)*4 + [0,4) of row l%32, so a direct 16-byte store touches 64 rows
+    // (cache lines) per instruction.  Where the stages have room, each wave
+    // instead writes its 32 rows x D block into LDS (16-byte chunk c of row r
+    // at chunk c ^ (r & 31), which spreads the 32 rows of one write over the
+    // banks) and stores whole rows: D*4 contiguous bytes per row, 1024/D rows
+    // an instruction.
+    constexpr int CHR = D / 4;  // 16-byte chunks in a row of D floats
+    if constexpr (NST * G::STAGE * 2 >= WAVES * ROWS_PER_WAVE * D * 4) {
         // every wave is past its last stage read (the loop ended with a barrier)
-        float *ob = reinterpret_cast<float *>(smem) + wave * (ROWS_PER_WAVE * DW);
+        float *ob = reinterpret_cast<float *>(smem) + wave * (ROWS_PER_WAVE * D);
 #pragma unroll
-        for (int dt = 0; dt < DW / 32; ++dt)
+        for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int c = dt * 8 + j * 2 + lhi;
                 const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
                                  acc_o[dt][j * 4 + 3] * sc};
-                *reinterpret_cast<f32x4 *>(ob + lrow * DW + ((c ^ (lrow & (CHR - 1) & 31)) << 2)) = v;
+                *reinterpret_cast<f32x4 *>(ob + lrow * D + ((c ^ (lrow & (CHR - 1) & 31)) << 2)) = v;
             }
         constexpr int RPI = 64 / CHR;  // rows per store instruction
         constexpr int NI = ROWS_PER_WAVE / RPI;
@@ -1347,14 +1127,14 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int r = i * RPI + sub;
-            rv[i] = *reinterpret_cast<const f32x4 *>(ob + r * DW + ((c ^ (r & (CHR - 1) & 31)) << 2));
+            rv[i] = *reinterpret_cast<const f32x4 *>(ob + r * D + ((c ^ (r & (CHR - 1) & 31)) << 2));
         }
         __builtin_amdgcn_sched_barrier(0);
         // lane r < 32 holds the destination (element offset) of row r of the
         // wave, -1 past the last row; a store takes its rows' offsets by lane
         // reads (scalar when one row fills the instruction)
         int64_t dst_off = -1;
-        if (row_ok) dst_off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + dh * DW;
+        if (row_ok) dst_off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
         const uint32_t off_lo = (uint32_t)dst_off, off_hi = (uint32_t)((uint64_t)dst_off >> 32);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -1377,9 +1157,9 @@ __global__ __launch_bounds__(64 * NW, (wg_per_cu<D, MASK, LD, NW>())) void paged
         }
     } else {
         if (!row_ok) return;
-        const int64_t off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D + dh * DW;
+        const int64_t off = (int64_t)(q_begin + tok) * p.out_stride + (int64_t)head * D;
 #pragma unroll
-        for (int dt = 0; dt < DW / 32; ++dt)
+        for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const f32x4 v = {acc_o[dt][j * 4] * sc, acc_o[dt][j * 4 + 1] * sc, acc_o[dt][j * 4 + 2] * sc,
@@ -1673,19 +1453,10 @@ hipError_t dispatch_pbf16(const KParams &kp, int mask, bool valid, bool qf32, hi
     }
 }
 
-// Row tiles at head_dim 256 with DMA staging run eight waves (two a SIMD, each
-// half of the output dims) when the host asks for it; otherwise four.
 template <int D, int MASK, int LD, bool QF32>
 hipError_t launch_kernel(const KParams &kp, hipStream_t stream) {
     const int grid = (kp.total_wg + 7) / 8 * 8;
-    if constexpr (D == 256 && LD == LD_DMA) {
-        if (kp.eight_waves) {
-            hipLaunchKernelGGL((paged_attn_kernel<D, MASK, LD, QF32, 2 * WAVES>), dim3(grid), dim3(128 * WAVES), 0,
-                               stream, kp);
-            return hipGetLastError();
-        }
-    }
-    hipLaunchKernelGGL((paged_attn_kernel<D, MASK, LD, QF32, WAVES>), dim3(grid), dim3(64 * WAVES), 0, stream, kp);
+    hipLaunchKernelGGL((paged_attn_kernel<D, MASK, LD, QF32>), dim3(grid), dim3(256), 0, stream, kp);
     return hipGetLastError();
 }
 
@@ -1846,17 +1617,13 @@ int run_attention(const emb_attn_args *a, int32_t nq_single, int32_t nk_single, 
     // Automatic choice: the key-split kernel reads every K/V tile once per 32
     // rows instead of once per 128, so it pays off only while the row tiles
     // would leave most of the GPU idle (at most half the CUs busy unsplit).
-    int n_cu = 0;
-    {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            n_cu = 0;
-    }
     bool ks_auto = false;
-    if (ks_ok && a->kernel == EMB_ATTN_AUTO && rows_per_unit <= 512 && n_cu > 0)
-        ks_auto = 2 * (int64_t)a->batch * a->hkv * kp.row_tiles <= n_cu;
-    kp.eight_waves = n_cu > 0 && kp.total_wg <= n_cu;
+    if (ks_ok && a->kernel == EMB_ATTN_AUTO && rows_per_unit <= 512) {
+        int dev = 0, n_cu = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+            ks_auto = 2 * (int64_t)a->batch * a->hkv * kp.row_tiles <= n_cu;
+    }
     if (ks_ok && (a->kernel == EMB_ATTN_KEY_SPLIT || ks_auto)) {
         KsParams ks{};
         ks.q = kp.q;
