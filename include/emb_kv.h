@@ -426,10 +426,8 @@ typedef struct emb_attn_args {
  * in how the work is cut.
  *   ROW_TILES: a workgroup owns 128 query rows of one (sequence, kv head) and
  *     shares every K/V tile among them; every mask kind, the valid-slot list,
- *     register or shadow staging, split-K.  At head_dim 256 with the shadow
- *     the workgroup runs eight waves (each with half of the output dims) when
- *     the grid fits one round on the compute units, four otherwise; both
- *     forms, and the register staging, give the same output bit for bit.
+ *     register or shadow staging, split-K (register and shadow staging give
+ *     the same output bit for bit).
  *   KEY_SPLIT: a workgroup owns 32 query rows and all their keys; its four
  *     waves split the keys and merge their partials in the kernel (no split-K
  *     workspace, no second launch).  FULL mask, f16 V shadow given, no
