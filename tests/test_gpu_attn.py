@@ -248,9 +248,7 @@ def test_multi_session_sweep(emb, orc, torch_dev, B, splits, split_keys):
     one batch are cut differently and the merge reads a count per session;
     a session with one split is written by its own workgroups (no partials)
     and skipped by the merge (split_keys 640 / 768 leave about half the
-    sessions unsplit).  Grids of more workgroups than the GPU has CUs (B = 64
-    with 2 or more splits) run the four-wave row tiles, the others the
-    eight-wave ones."""
+    sessions unsplit)."""
     torch, dev = torch_dev
     lens = [300 + orc.lib().orc_mt64_nth(0xE3BD0004, b + 1) % 901 for b in range(B)]
     assert 300 <= min(lens) and max(lens) <= 1200

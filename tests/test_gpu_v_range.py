@@ -185,10 +185,10 @@ def test_faces_any_v_range(emb, orc, torch_dev, name, vs):
 
 def test_dim_halves_of_different_magnitude(emb, orc, torch_dev):
     """V dims [0, 128) scaled by 1e-2 and dims [128, 256) by 1e3 (cfg1-like
-    shape, split-K 1 and 3).  The head_dim-256 row tiles give each half of the
-    output dims to its own wave, and split partials carry a power-of-two scale
-    per half (2^17 apart here): each half is held to the bar relative to its
-    own magnitude, so a half merged with the other half's scale would fail."""
+    shape, split-K 1 and 3).  Split partials carry a power-of-two scale per
+    half of the dims (2^17 apart here): each half is held to the bar relative
+    to its own magnitude, so a half merged with the other half's scale would
+    fail."""
     torch, dev = torch_dev
     rng = np.random.default_rng(0xD1A5)
     dscale = np.concatenate([np.full(128, 1e-2), np.full(128, 1e3)])[None, None, :]
